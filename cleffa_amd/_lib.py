@@ -1,0 +1,90 @@
+"""ctypes binding of libclef_hip_attn.so (the C ABI declared in include/clef_hip_attn.h).
+
+The library is the product: there is no Python or CPU fallback. Loading fails loudly when the
+shared library has not been built.
+"""
+import ctypes
+from ctypes import POINTER, c_bool, c_char_p, c_float, c_int, c_int32, c_size_t, c_uint16, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libclef_hip_attn.so"
+
+OUT_BF16, OUT_F16, OUT_F32 = 0, 1, 2
+BLOCK_Q = 128
+KV_ALIGN = 64
+BLOCK_INTS = 8
+
+# Every symbol include/clef_hip_attn.h declares.
+EXPORTS = (
+    "clef_hip_attn_version", "clef_hip_attn_wave_size", "clef_hip_attn_init",
+    "clef_hip_attn_plan_max_blocks", "clef_hip_attn_plan_max_kv_rows", "clef_hip_attn_plan",
+    "clef_hip_rope_inv_freq", "clef_hip_vis_positions", "clef_hip_attn_prep_kv",
+    "clef_hip_attn_core", "clef_hip_attn_prefill", "clef_hip_vis_attention",
+)
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("nh", c_int), ("nkv", c_int), ("hd", c_int), ("n_rot", c_int),
+        ("eps", c_float), ("scale", c_float),
+        ("T", c_int), ("row", c_int),
+        ("qkv", c_void_p), ("q_norm", c_void_p), ("k_norm", c_void_p), ("pos3", c_void_p),
+        ("inv_freq", c_void_p), ("k_plane", c_void_p), ("vt_plane", c_void_p),
+        ("kvT", c_int), ("blocks", c_void_p), ("n_blk", c_int), ("kv_tok", c_void_p),
+        ("kv_rows", c_int), ("causal", c_int), ("gate", c_int),
+        ("out", c_void_p), ("out_type", c_int), ("f16_lim", c_float), ("ovf", c_void_p),
+    ]
+
+
+class VisArgs(ctypes.Structure):
+    _fields_ = [
+        ("P", c_int), ("heads", c_int), ("hd", c_int), ("scale", c_float),
+        ("qkv", c_void_p), ("bias", c_void_p), ("pos2", c_void_p), ("inv_freq", c_void_p),
+        ("q_plane", c_void_p), ("k_plane", c_void_p), ("vt_plane", c_void_p), ("kvT", c_int),
+        ("blocks", c_void_p), ("n_blk", c_int), ("kv_tok", c_void_p), ("kv_rows", c_int),
+        ("out", c_void_p), ("out_type", c_int), ("f16_lim", c_float), ("ovf", c_void_p),
+    ]
+
+
+_lib = None
+
+
+def load():
+    """Returns the loaded library; raises if it is missing (no fallback path exists)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is not built: run `python -m cleffa_amd.build` "
+                           "(hipcc --offload-arch=gfx950); there is no CPU fallback")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    lib.clef_hip_attn_version.restype = c_int
+    lib.clef_hip_attn_wave_size.restype = c_int
+    lib.clef_hip_attn_init.argtypes = [c_char_p, c_size_t]
+    lib.clef_hip_attn_init.restype = c_bool
+    lib.clef_hip_attn_plan_max_blocks.argtypes = [c_int, c_int]
+    lib.clef_hip_attn_plan_max_blocks.restype = c_int
+    lib.clef_hip_attn_plan_max_kv_rows.argtypes = [c_int, c_int]
+    lib.clef_hip_attn_plan_max_kv_rows.restype = c_int
+    lib.clef_hip_attn_plan.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int, c_int,
+                                       POINTER(c_int32), c_int, POINTER(c_int32), c_int,
+                                       POINTER(c_int), POINTER(c_int), c_char_p, c_size_t]
+    lib.clef_hip_attn_plan.restype = c_bool
+    lib.clef_hip_rope_inv_freq.argtypes = [c_float, c_int, POINTER(c_float)]
+    lib.clef_hip_rope_inv_freq.restype = None
+    lib.clef_hip_vis_positions.argtypes = [POINTER(c_int32), c_int, POINTER(c_int32), c_int,
+                                           POINTER(c_int32), c_char_p, c_size_t]
+    lib.clef_hip_vis_positions.restype = c_bool
+    for name in ("clef_hip_attn_prep_kv", "clef_hip_attn_core", "clef_hip_attn_prefill"):
+        fn = getattr(lib, name)
+        fn.argtypes = [POINTER(AttnArgs), c_void_p, c_char_p, c_size_t]
+        fn.restype = c_bool
+    lib.clef_hip_vis_attention.argtypes = [POINTER(VisArgs), c_void_p, c_char_p, c_size_t]
+    lib.clef_hip_vis_attention.restype = c_bool
+    _lib = lib
+    return lib
+
+
+def check(ok, err):
+    if not ok:
+        raise RuntimeError(err.value.decode(errors="replace") or "hip: unknown error")

@@ -1,0 +1,289 @@
+"""Host-side layer above the C ABI: plans, plane allocation and the attention calls.
+
+This mirrors what cleffa's Metal backend does around its attention kernels:
+
+* ``AttnPlan`` is the per-pass block list and kv-row map (clef_metal.m:1243-1257, built once per
+  forward from seq_bounds; clef.c:470-497 packs the records);
+* ``TextAttention.forward`` is one full-attention layer, the call that replaces
+  ``encode_attention_tu`` (clef_metal.m:829-882) and the FP32 branch (clef_metal.m:1330-1413);
+* ``VisionAttention.forward`` replaces the vision loop's vis_qkv_rope + vis_attention_mma/_mpp
+  dispatches (clef_metal.m:1022-1049), here with all images packed in one launch via cu_seqlens.
+
+torch provides device memory and the stream; every computation runs in libclef_hip_attn.so.
+Shapes and dtypes are checked here, on the host, before any launch.
+"""
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import AttnArgs, VisArgs, OUT_BF16, OUT_F16, OUT_F32, BLOCK_INTS
+
+_OUT_TYPES = {"bf16": (OUT_BF16, torch.bfloat16), "f16": (OUT_F16, torch.float16),
+              "f32": (OUT_F32, torch.float32)}
+
+
+def _i32p(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+
+def _err():
+    return ctypes.create_string_buffer(512)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _device(device):
+    """torch.device with an explicit index for cuda ("cuda" -> "cuda:<current>")."""
+    d = torch.device(device)
+    if d.type == "cuda" and d.index is None:
+        d = torch.device("cuda", torch.cuda.current_device())
+    return d
+
+
+def _stream_handle(stream):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+_initialised = set()
+
+
+def init_device(device=None):
+    """clef_hip_attn_init on the given (or current) device, once per device."""
+    lib = _lib.load()
+    dev = _device("cuda" if device is None else device)
+    if dev.index in _initialised:
+        return
+    with torch.cuda.device(dev):
+        err = _err()
+        _lib.check(lib.clef_hip_attn_init(err, len(err)), err)
+    _initialised.add(dev.index)
+
+
+def rope_inv_freq(theta, n_rot):
+    """f32 table 1/theta^(2j/n_rot), j < n_rot/2, computed by the library (clef_metal.m:176-192)."""
+    lib = _lib.load()
+    out = np.zeros(max(n_rot // 2, 1), dtype=np.float32)
+    lib.clef_hip_rope_inv_freq(ctypes.c_float(theta), n_rot,
+                               out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    return out[: n_rot // 2]
+
+
+def vision_positions(cu_seqlens, grid_w, merge=2):
+    """[P][2] (grid row, grid column) of every patch, merge-window order (metal/clef.metal:1639-1641)."""
+    lib = _lib.load()
+    cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+    gw = np.ascontiguousarray(grid_w, dtype=np.int32)
+    n = len(cu) - 1
+    if len(gw) != n:
+        raise ValueError("grid_w needs one entry per image")
+    pos2 = np.zeros((max(int(cu[-1]), 1), 2), dtype=np.int32)
+    err = _err()
+    _lib.check(lib.clef_hip_vis_positions(_i32p(cu), n, _i32p(gw), merge, _i32p(pos2), err, len(err)), err)
+    return pos2[: int(cu[-1])]
+
+
+class AttnPlan:
+    """Query blocks and kv rows of one pass (host arrays plus their device copies).
+
+    cu_q: record bounds over the pass rows (int32, cu_q[0] = 0).
+    cu_k: None for a fresh pass; for a prefix-cache pass the records' kv-row bounds, each
+          record's cached keys first and its new tokens last (cu_k[r] multiples of 8).
+    """
+
+    def __init__(self, cu_q, cu_k=None, causal=True, device="cuda"):
+        lib = _lib.load()
+        cu_q = np.ascontiguousarray(cu_q, dtype=np.int32)
+        self.n_seq = len(cu_q) - 1
+        self.T = int(cu_q[-1])
+        self.cu_q = cu_q
+        self.cu_k = None if cu_k is None else np.ascontiguousarray(cu_k, dtype=np.int32)
+        if self.cu_k is not None and len(self.cu_k) != len(cu_q):
+            raise ValueError("cu_seqlens_k must have as many entries as cu_seqlens_q")
+        self.causal = bool(causal)
+        tk = self.T if self.cu_k is None else int(self.cu_k[-1])
+        max_blk = lib.clef_hip_attn_plan_max_blocks(self.n_seq, self.T)
+        max_kv = lib.clef_hip_attn_plan_max_kv_rows(self.n_seq, tk)
+        blocks = np.zeros((max(max_blk, 1), BLOCK_INTS), dtype=np.int32)
+        kv_tok = np.zeros(max(max_kv, 1), dtype=np.int32)
+        n_blk, kv_rows = ctypes.c_int(0), ctypes.c_int(0)
+        err = _err()
+        ok = lib.clef_hip_attn_plan(_i32p(cu_q), None if self.cu_k is None else _i32p(self.cu_k),
+                                    self.n_seq, int(self.causal), _i32p(blocks), max_blk,
+                                    _i32p(kv_tok), max_kv, ctypes.byref(n_blk), ctypes.byref(kv_rows),
+                                    err, len(err))
+        _lib.check(ok, err)
+        self.n_blk = n_blk.value
+        self.kv_rows = kv_rows.value
+        self.blocks_host = blocks[: self.n_blk].copy()
+        self.kv_tok_host = kv_tok[: self.kv_rows].copy()
+        self.device = _device(device)
+        self.blocks = torch.from_numpy(np.ascontiguousarray(blocks[: max(self.n_blk, 1)])).to(self.device)
+        self.kv_tok = torch.from_numpy(np.ascontiguousarray(kv_tok[: max(self.kv_rows, 1)])).to(self.device)
+        # kv rows the planes must hold, rounded to the 16-byte V^T chunk
+        self.kvT = max(8, (self.kv_rows + 7) // 8 * 8)
+
+    def pairs(self):
+        """(query, key) pairs the plan visits under its mask: the algorithmic work unit."""
+        total = 0
+        for r in range(self.n_seq):
+            nq = int(self.cu_q[r + 1] - self.cu_q[r])
+            nk = nq if self.cu_k is None else int(self.cu_k[r + 1] - self.cu_k[r])
+            L = nk - nq
+            total += nq * L + nq * (nq + 1) // 2 if self.causal else nq * nk
+        return total
+
+
+def _check(t, name, shape, dtype, device):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch tensor")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.data_ptr() % 16:
+        raise ValueError(f"{name} must be 16-byte aligned")
+
+
+class TextAttention:
+    """One gated full-attention layer of the dense Clef models (hd 256, GQA)."""
+
+    def __init__(self, nh, nkv, hd=256, n_rot=64, eps=1e-6, rope_theta=1e7, device="cuda"):
+        self.nh, self.nkv, self.hd, self.n_rot, self.eps = nh, nkv, hd, n_rot, eps
+        self.scale = 1.0 / math.sqrt(hd)
+        self.row = 2 * nh * hd + 2 * nkv * hd
+        self.device = _device(device)
+        init_device(self.device)
+        self.inv_freq = torch.from_numpy(rope_inv_freq(rope_theta, n_rot).copy()).to(self.device) \
+            if n_rot else torch.zeros(1, dtype=torch.float32, device=self.device)
+
+    def planes(self, kvT):
+        """K plane [nkv][kvT][hd] and V^T plane [nkv][hd][kvT] (bf16)."""
+        k = torch.empty((self.nkv, kvT, self.hd), dtype=torch.bfloat16, device=self.device)
+        vt = torch.empty((self.nkv, self.hd, kvT), dtype=torch.bfloat16, device=self.device)
+        return k, vt
+
+    def args(self, qkv, q_norm, k_norm, pos3, plan, out, k_plane, vt_plane, kvT,
+             out_type=OUT_BF16, gate=True, ovf=None, f16_lim=65504.0):
+        T = plan.T
+        dev = self.device
+        _check(qkv, "qkv", (T, qkv.shape[1] if qkv.dim() == 2 else -1), torch.bfloat16, dev)
+        if qkv.shape[1] < self.row or qkv.shape[1] % 8:
+            raise ValueError(f"qkv row {qkv.shape[1]} must be >= {self.row} and a multiple of 8")
+        if (q_norm is None) != (k_norm is None):
+            raise ValueError("q_norm and k_norm must both be given or both be None")
+        if q_norm is not None:
+            _check(q_norm, "q_norm", (self.hd,), torch.float32, dev)
+            _check(k_norm, "k_norm", (self.hd,), torch.float32, dev)
+        if self.n_rot:
+            _check(pos3, "pos3", (T, 3), torch.int32, dev)
+        _check(k_plane, "k_plane", (self.nkv, kvT, self.hd), torch.bfloat16, dev)
+        _check(vt_plane, "vt_plane", (self.nkv, self.hd, kvT), torch.bfloat16, dev)
+        if kvT < plan.kv_rows or kvT % 8:
+            raise ValueError(f"kvT {kvT} must be >= {plan.kv_rows} and a multiple of 8")
+        _check(out, "out", (T, self.nh * self.hd), {OUT_BF16: torch.bfloat16, OUT_F16: torch.float16,
+                                                    OUT_F32: torch.float32}[out_type], dev)
+        if ovf is not None:
+            _check(ovf, "ovf", (T,), torch.int32, dev)
+        if plan.device != dev:
+            raise ValueError("plan lives on another device")
+        if plan.n_blk:
+            b = plan.blocks_host
+            if int((b[:, 0] + b[:, 1]).max()) > T or int((b[:, 3] + b[:, 4]).max()) > kvT:
+                raise ValueError("plan does not fit the pass rows / planes")
+        a = AttnArgs()
+        a.nh, a.nkv, a.hd, a.n_rot = self.nh, self.nkv, self.hd, self.n_rot
+        a.eps, a.scale = self.eps, self.scale
+        a.T, a.row = T, qkv.shape[1]
+        a.qkv, a.q_norm, a.k_norm = _ptr(qkv), _ptr(q_norm), _ptr(k_norm)
+        a.pos3, a.inv_freq = _ptr(pos3), _ptr(self.inv_freq)
+        a.k_plane, a.vt_plane, a.kvT = _ptr(k_plane), _ptr(vt_plane), kvT
+        a.blocks, a.n_blk = _ptr(plan.blocks), plan.n_blk
+        a.kv_tok, a.kv_rows = _ptr(plan.kv_tok), plan.kv_rows
+        a.causal, a.gate = int(plan.causal), int(gate)
+        a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
+        return a
+
+    def forward(self, qkv, q_norm, k_norm, pos3, plan, out=None, out_dtype="bf16", gate=True,
+                k_plane=None, vt_plane=None, kvT=None, ovf=None, f16_lim=65504.0, stream=None,
+                stage="prefill"):
+        """Runs one layer's attention. stage: "prefill" (prep_kv + core), "prep", or "core"."""
+        lib = _lib.load()
+        out_type, odt = _OUT_TYPES[out_dtype]
+        if out is None:
+            out = torch.empty((plan.T, self.nh * self.hd), dtype=odt, device=self.device)
+        if k_plane is None:
+            kvT = plan.kvT
+            k_plane, vt_plane = self.planes(kvT)
+        elif kvT is None:
+            kvT = k_plane.shape[1]
+        a = self.args(qkv, q_norm, k_norm, pos3, plan, out, k_plane, vt_plane, kvT,
+                      out_type=out_type, gate=gate, ovf=ovf, f16_lim=f16_lim)
+        fn = {"prefill": lib.clef_hip_attn_prefill, "prep": lib.clef_hip_attn_prep_kv,
+              "core": lib.clef_hip_attn_core}[stage]
+        err = _err()
+        _lib.check(fn(ctypes.byref(a), _stream_handle(stream), err, len(err)), err)
+        return out
+
+
+class VisionAttention:
+    """Vision tower attention: hd 72, MHA, bidirectional within each image, 2-D rotary."""
+
+    HDK = 80
+
+    def __init__(self, heads=16, hd=72, theta=10000.0, device="cuda"):
+        self.heads, self.hd = heads, hd
+        self.E = heads * hd
+        self.scale = 1.0 / math.sqrt(hd)
+        self.device = _device(device)
+        init_device(self.device)
+        self.inv_freq = torch.from_numpy(rope_inv_freq(theta, hd // 2).copy()).to(self.device)
+
+    def forward(self, qkv, bias, pos2, plan, out=None, out_dtype="bf16", ovf=None,
+                f16_lim=65504.0, stream=None, scratch=None):
+        lib = _lib.load()
+        if plan.causal or plan.cu_k is not None:
+            raise ValueError("vision attention takes a bidirectional fresh plan")
+        P, dev = plan.T, self.device
+        _check(qkv, "qkv", (P, 3 * self.E), torch.bfloat16, dev)
+        if bias is not None:
+            _check(bias, "bias", (3 * self.E,), torch.float32, dev)
+        _check(pos2, "pos2", (P, 2), torch.int32, dev)
+        out_type, odt = _OUT_TYPES[out_dtype]
+        if out is None:
+            out = torch.empty((P, self.E), dtype=odt, device=dev)
+        _check(out, "out", (P, self.E), odt, dev)
+        if ovf is not None:
+            _check(ovf, "ovf", (P,), torch.int32, dev)
+        kvT = plan.kvT
+        if scratch is None:
+            scratch = self.scratch(P, kvT)
+        q_plane, k_plane, vt_plane = scratch
+        _check(q_plane, "q_plane", (self.heads, P, self.HDK), torch.bfloat16, dev)
+        _check(k_plane, "k_plane", (self.heads, kvT, self.HDK), torch.bfloat16, dev)
+        _check(vt_plane, "vt_plane", (self.heads, self.hd, kvT), torch.bfloat16, dev)
+        a = VisArgs()
+        a.P, a.heads, a.hd, a.scale = P, self.heads, self.hd, self.scale
+        a.qkv, a.bias, a.pos2, a.inv_freq = _ptr(qkv), _ptr(bias), _ptr(pos2), _ptr(self.inv_freq)
+        a.q_plane, a.k_plane, a.vt_plane, a.kvT = _ptr(q_plane), _ptr(k_plane), _ptr(vt_plane), kvT
+        a.blocks, a.n_blk, a.kv_tok, a.kv_rows = _ptr(plan.blocks), plan.n_blk, _ptr(plan.kv_tok), plan.kv_rows
+        a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
+        err = _err()
+        _lib.check(lib.clef_hip_vis_attention(ctypes.byref(a), _stream_handle(stream), err, len(err)), err)
+        return out
+
+    def scratch(self, P, kvT):
+        dev = self.device
+        return (torch.empty((self.heads, max(P, 1), self.HDK), dtype=torch.bfloat16, device=dev),
+                torch.empty((self.heads, kvT, self.HDK), dtype=torch.bfloat16, device=dev),
+                torch.empty((self.heads, self.hd, kvT), dtype=torch.bfloat16, device=dev))

@@ -1,0 +1,251 @@
+// C ABI of the prefill attention path: argument checks, the host-side plan builder and the
+// kernel launches. Declarations and layouts are documented in include/clef_hip_attn.h.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "attn_kernels.h"
+#include "attn_params.h"
+#include "clef_hip_attn.h"
+
+using namespace clef_hip;
+
+namespace {
+
+constexpr int kVersion = 1;
+constexpr int kVisHD = 72, kVisHDK = 80;
+
+bool fail(char *err, size_t errlen, const char *fmt, ...) {
+    if (err && errlen) {
+        int n = snprintf(err, errlen, "hip: ");
+        if (n < 0) n = 0;
+        if ((size_t)n < errlen) {
+            va_list ap;
+            va_start(ap, fmt);
+            vsnprintf(err + n, errlen - (size_t)n, fmt, ap);
+            va_end(ap);
+        }
+    }
+    return false;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool launch_ok(const char *what, char *err, size_t errlen) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(err, errlen, "%s launch failed: %s", what, hipGetErrorString(e));
+    return true;
+}
+
+bool rot_ok(int n_rot, int hd) {
+    return (n_rot == 0 || n_rot == 32 || n_rot == 64 || n_rot == 128 || n_rot == 256) && n_rot <= hd;
+}
+
+bool check_text(const clef_hip_attn_args *a, bool need_core, char *err, size_t errlen) {
+    if (!a) return fail(err, errlen, "null attention arguments");
+    if (a->hd != 256) return fail(err, errlen, "text attention supports hd 256 only (got %d)", a->hd);
+    if (a->nh <= 0 || a->nkv <= 0 || a->nh % a->nkv) return fail(err, errlen, "bad head counts nh=%d nkv=%d", a->nh, a->nkv);
+    if (!rot_ok(a->n_rot, a->hd)) return fail(err, errlen, "unsupported n_rot %d", a->n_rot);
+    if (a->T < 0 || a->n_blk < 0 || a->kv_rows < 0) return fail(err, errlen, "negative sizes");
+    const long need_row = 2L * a->nh * a->hd + 2L * a->nkv * a->hd;
+    if (a->row < need_row || a->row % 8) return fail(err, errlen, "qkv row %d must be >= %ld and a multiple of 8", a->row, need_row);
+    if (a->kvT % 8 || a->kvT < a->kv_rows) return fail(err, errlen, "kvT %d must be a multiple of 8 and >= kv_rows %d", a->kvT, a->kv_rows);
+    if (!a->qkv || !aligned16(a->qkv)) return fail(err, errlen, "qkv must be a 16-byte aligned device pointer");
+    if (!aligned16(a->k_norm) || !aligned16(a->q_norm)) return fail(err, errlen, "norm weights must be 16-byte aligned");
+    if (!a->k_norm != !a->q_norm) return fail(err, errlen, "q_norm and k_norm must both be set or both be NULL");
+    if (a->n_rot && (!a->pos3 || !a->inv_freq)) return fail(err, errlen, "rotary needs pos3 and inv_freq");
+    if (!a->k_plane || !aligned16(a->k_plane) || !a->vt_plane || !aligned16(a->vt_plane)) return fail(err, errlen, "K / V^T planes must be 16-byte aligned");
+    if (need_core) {
+        if (a->n_blk && !a->blocks) return fail(err, errlen, "missing block list");
+        if (!a->out || !aligned16(a->out)) return fail(err, errlen, "out must be a 16-byte aligned device pointer");
+        if (a->out_type < CLEF_HIP_OUT_BF16 || a->out_type > CLEF_HIP_OUT_F32) return fail(err, errlen, "bad out_type %d", a->out_type);
+        if (!(a->scale > 0.f)) return fail(err, errlen, "bad scale");
+    } else if (a->kv_rows && !a->kv_tok) {
+        return fail(err, errlen, "missing kv_tok");
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int clef_hip_attn_version(void) { return kVersion; }
+int clef_hip_attn_wave_size(void) { return 64; }
+
+bool clef_hip_attn_init(char *err, size_t errlen) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(err, errlen, "no device: %s", hipGetErrorString(e));
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return fail(err, errlen, "device query failed: %s", hipGetErrorString(e));
+    if (!strstr(prop.gcnArchName, "gfx950")) return fail(err, errlen, "kernels are built for gfx950, device is %s", prop.gcnArchName);
+    if (prop.warpSize != 64) return fail(err, errlen, "attention kernels need 64-wide wavefronts (device reports %d)", prop.warpSize);
+    const size_t need = sizeof(uint16_t) * 2 * AttnCfg<256, 64, true>::STAGE;
+    if (prop.sharedMemPerBlock < need) return fail(err, errlen, "device LDS %zu < %zu bytes", (size_t)prop.sharedMemPerBlock, need);
+    return true;
+}
+
+int clef_hip_attn_plan_max_blocks(int n_seq, int Tq) {
+    if (n_seq < 0 || Tq < 0) return 0;
+    return Tq / CLEF_HIP_BLOCK_Q + n_seq + 1;
+}
+
+int clef_hip_attn_plan_max_kv_rows(int n_seq, int Tk) {
+    if (n_seq < 0 || Tk < 0) return 0;
+    return Tk + CLEF_HIP_KV_ALIGN * (n_seq + 1);
+}
+
+bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int causal,
+                        int32_t *blocks, int max_blocks, int32_t *kv_tok, int max_kv,
+                        int *n_blk, int *kv_rows, char *err, size_t errlen) {
+    if (!cu_q || n_seq < 0 || !n_blk || !kv_rows) return fail(err, errlen, "bad plan arguments");
+    if (cu_q[0] != 0) return fail(err, errlen, "cu_seqlens_q must start at 0");
+    if (cu_k && cu_k[0] != 0) return fail(err, errlen, "cu_seqlens_k must start at 0");
+    struct Ent { int32_t v[CLEF_HIP_BLOCK_INTS]; };
+    std::vector<Ent> ents;
+    int kv_off = 0;
+    for (int r = 0; r < n_seq; r++) {
+        const int nq = cu_q[r + 1] - cu_q[r];
+        if (nq < 0) return fail(err, errlen, "cu_seqlens_q decreases at record %d", r);
+        int nk = nq, k0 = kv_off;
+        if (cu_k) {
+            nk = cu_k[r + 1] - cu_k[r];
+            k0 = cu_k[r];
+            if (nk < nq) return fail(err, errlen, "record %d has %d keys for %d queries", r, nk, nq);
+            if (k0 % 8) return fail(err, errlen, "cu_seqlens_k[%d] = %d is not a multiple of 8", r, k0);
+        } else {
+            kv_off += (nq + CLEF_HIP_KV_ALIGN - 1) / CLEF_HIP_KV_ALIGN * CLEF_HIP_KV_ALIGN;
+        }
+        const int L = nk - nq;
+        for (int i0 = 0; i0 < nq; i0 += CLEF_HIP_BLOCK_Q) {
+            Ent e;
+            const int n = std::min(CLEF_HIP_BLOCK_Q, nq - i0);
+            e.v[0] = cu_q[r] + i0;
+            e.v[1] = n;
+            e.v[2] = L + i0;
+            e.v[3] = k0;
+            e.v[4] = causal ? std::min(nk, L + i0 + n) : nk;
+            e.v[5] = cu_q[r];
+            e.v[6] = r;
+            e.v[7] = 0;
+            ents.push_back(e);
+        }
+    }
+    const int total_kv = cu_k ? cu_k[n_seq] : kv_off;
+    if ((int)ents.size() > max_blocks) return fail(err, errlen, "plan needs %zu blocks, room for %d", ents.size(), max_blocks);
+    if (total_kv > max_kv) return fail(err, errlen, "plan needs %d kv rows, room for %d", total_kv, max_kv);
+    if ((!blocks && !ents.empty()) || (!kv_tok && total_kv)) return fail(err, errlen, "missing plan output arrays");
+    // Longest key range first, so the long causal blocks start early (clef_metal.m:1243-1257
+    // orders each record's blocks longest first; here the order is global across records).
+    std::stable_sort(ents.begin(), ents.end(), [](const Ent &x, const Ent &y) { return x.v[4] > y.v[4]; });
+    for (size_t i = 0; i < ents.size(); i++) memcpy(blocks + CLEF_HIP_BLOCK_INTS * i, ents[i].v, sizeof(ents[i].v));
+    for (int i = 0; i < total_kv; i++) kv_tok[i] = -1;
+    kv_off = 0;
+    for (int r = 0; r < n_seq; r++) {
+        const int nq = cu_q[r + 1] - cu_q[r];
+        const int nk = cu_k ? cu_k[r + 1] - cu_k[r] : nq;
+        const int k0 = cu_k ? cu_k[r] : kv_off;
+        for (int j = 0; j < nq; j++) kv_tok[k0 + (nk - nq) + j] = cu_q[r] + j;
+        if (!cu_k) kv_off += (nq + CLEF_HIP_KV_ALIGN - 1) / CLEF_HIP_KV_ALIGN * CLEF_HIP_KV_ALIGN;
+    }
+    *n_blk = (int)ents.size();
+    *kv_rows = total_kv;
+    return true;
+}
+
+void clef_hip_rope_inv_freq(float theta, int n_rot, float *inv_freq) {
+    for (int j = 0; j < n_rot / 2; j++) inv_freq[j] = 1.0f / powf(theta, (float)(2 * j) / (float)n_rot);
+}
+
+bool clef_hip_vis_positions(const int32_t *cu, int n_img, const int32_t *grid_w, int merge,
+                            int32_t *pos2, char *err, size_t errlen) {
+    if (!cu || !grid_w || !pos2 || n_img < 0 || merge <= 0) return fail(err, errlen, "bad vision position arguments");
+    for (int g = 0; g < n_img; g++) {
+        const int P = cu[g + 1] - cu[g];
+        if (P < 0 || grid_w[g] <= 0 || grid_w[g] % merge) return fail(err, errlen, "bad image %d geometry", g);
+        const int window = merge * merge, w2 = grid_w[g] / merge;
+        for (int p = 0; p < P; p++) {
+            const int blk = p / window, within = p % window;
+            pos2[2 * (cu[g] + p)] = (blk / w2) * merge + within / merge;
+            pos2[2 * (cu[g] + p) + 1] = (blk % w2) * merge + within % merge;
+        }
+    }
+    return true;
+}
+
+bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {
+    if (!check_text(a, false, err, errlen)) return false;
+    if (a->kv_rows == 0) return true;
+    PrepParams p;
+    p.qkv = a->qkv; p.k_norm = a->k_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
+    p.kv_tok = a->kv_tok; p.k_plane = a->k_plane; p.vt_plane = a->vt_plane;
+    p.row = a->row; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
+    p.kv_rows = a->kv_rows; p.eps = a->eps;
+    dim3 grid((a->kv_rows + 63) / 64, a->nkv);
+    hipLaunchKernelGGL(text_prep_kv_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
+    return launch_ok("text_prep_kv", err, errlen);
+}
+
+bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {
+    if (!check_text(a, true, err, errlen)) return false;
+    if (a->n_blk == 0) return true;
+    AttnParams p;
+    memset(&p, 0, sizeof(p));
+    p.qkv = a->qkv; p.q_norm = a->q_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
+    p.k_plane = a->k_plane; p.vt_plane = a->vt_plane; p.blocks = a->blocks;
+    p.out = a->out; p.ovf = a->ovf;
+    p.row = a->row; p.T = a->T; p.kvT = a->kvT; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot;
+    p.eps = a->eps; p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = a->f16_lim;
+    p.causal = a->causal ? 1 : 0; p.gate = a->gate ? 1 : 0; p.out_type = a->out_type;
+    p.out_ld = a->nh * a->hd;
+    const long grid = (long)a->n_blk * a->nh;
+    if (grid > 0x7fffffffL) return fail(err, errlen, "grid too large");
+    hipLaunchKernelGGL((attn_fwd_kernel<256, 64, true>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+    return launch_ok("attn_fwd<256>", err, errlen);
+}
+
+bool clef_hip_attn_prefill(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {
+    if (!check_text(a, true, err, errlen)) return false;
+    if (!clef_hip_attn_prep_kv(a, stream, err, errlen)) return false;
+    return clef_hip_attn_core(a, stream, err, errlen);
+}
+
+bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen) {
+    if (!a) return fail(err, errlen, "null vision arguments");
+    if (a->hd != kVisHD) return fail(err, errlen, "vision attention supports hd 72 only (got %d)", a->hd);
+    if (a->P < 0 || a->heads <= 0 || a->n_blk < 0 || a->kv_rows < 0) return fail(err, errlen, "bad vision sizes");
+    if (a->kvT % 8 || a->kvT < a->kv_rows) return fail(err, errlen, "kvT %d must be a multiple of 8 and >= kv_rows %d", a->kvT, a->kv_rows);
+    if (!a->qkv || !a->pos2 || !a->inv_freq || !a->q_plane || !a->k_plane || !a->vt_plane || !a->out)
+        return fail(err, errlen, "missing vision buffer");
+    if (!aligned16(a->q_plane) || !aligned16(a->k_plane) || !aligned16(a->vt_plane) || !aligned16(a->out))
+        return fail(err, errlen, "vision planes and output must be 16-byte aligned");
+    if (a->out_type < CLEF_HIP_OUT_BF16 || a->out_type > CLEF_HIP_OUT_F32) return fail(err, errlen, "bad out_type %d", a->out_type);
+    if ((a->n_blk && !a->blocks) || (a->kv_rows && !a->kv_tok)) return fail(err, errlen, "missing plan");
+    if (a->kv_rows) {
+        VisPrepParams q;
+        q.qkv = a->qkv; q.bias = a->bias; q.pos2 = a->pos2; q.inv_freq = a->inv_freq; q.kv_tok = a->kv_tok;
+        q.q_plane = a->q_plane; q.k_plane = a->k_plane; q.vt_plane = a->vt_plane;
+        q.P = a->P; q.heads = a->heads; q.kvT = a->kvT; q.kv_rows = a->kv_rows;
+        hipLaunchKernelGGL(vis_prep_kernel, dim3((a->kv_rows + 63) / 64, a->heads), dim3(256), 0, (hipStream_t)stream, q);
+        if (!launch_ok("vis_prep", err, errlen)) return false;
+    }
+    if (a->n_blk == 0) return true;
+    AttnParams p;
+    memset(&p, 0, sizeof(p));
+    p.q_plane = a->q_plane; p.k_plane = a->k_plane; p.vt_plane = a->vt_plane; p.blocks = a->blocks;
+    p.out = a->out; p.ovf = a->ovf;
+    p.T = a->P; p.kvT = a->kvT; p.nh = a->heads; p.nkv = a->heads;
+    p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = a->f16_lim;
+    p.causal = 0; p.gate = 0; p.out_type = a->out_type; p.out_ld = a->heads * kVisHD;
+    (void)kVisHDK;
+    hipLaunchKernelGGL((attn_fwd_kernel<72, 64, false>), dim3((unsigned)(a->n_blk * a->heads)), dim3(256), 0, (hipStream_t)stream, p);
+    return launch_ok("attn_fwd<72>", err, errlen);
+}
+
+}  // extern "C"

@@ -1,0 +1,533 @@
+// Prefill attention kernels for CDNA4 (gfx950): packed varlen causal GQA attention over
+// record-aligned query blocks, with the Q prologue (per-head RMSNorm + partial rotary) fused
+// into the attention kernel and the sigmoid output gate fused into its epilogue, a K/V
+// prologue kernel that writes the K and V^T planes, and the vision tower's prologue
+// (bias + 2-D rotary) feeding the same attention kernel at head dim 72.
+//
+// Semantics follow cleffa's attention family (metal/clef.metal:245-300 attn_prep,
+// metal/clef.metal:930-1093 attention_tu, metal/clef.metal:657-849 prefix variant,
+// metal/clef.metal:1616-1964 vision), restated for 64-wide wavefronts and bf16 MFMA.
+//
+// Compute layout (per workgroup = 4 wavefronts, one query block of 128 rows of one q head):
+//   S^T = K . Q^T      v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = Q held in VGPRs.
+//                      Each lane ends up owning one query column and 32 keys of a 64-key tile,
+//                      so the row max / row sum need one cross-half exchange only.
+//   O^T += V^T . P^T   A = V^T rows from LDS (V is stored transposed in HBM by the prologue),
+//                      B = bf16 P straight from the softmax registers (no LDS round trip).
+// The A-operand rows of both products are read in a bit-permuted order (bits 2 and 3 of the
+// row index swapped) so that the MFMA output rows a lane owns are 8 consecutive keys / dims:
+// P feeds the next product without shuffles and the epilogue stores 16-byte runs.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attn_params.h"
+
+namespace clef_hip {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
+
+__device__ __forceinline__ float bf_lo(unsigned w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((unsigned)b << 16); }
+
+// Round-to-nearest-even pair conversion (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ unsigned pack_bf16(float a, float b) {
+    bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(unsigned, v);
+}
+__device__ __forceinline__ uint16_t f2bf(float a) {
+    __bf16 v = (__bf16)a;
+    return __builtin_bit_cast(uint16_t, v);
+}
+
+// Row permutation of the MFMA A operand: swap bits 2 and 3.
+__device__ __forceinline__ int perm_row(int r) {
+    return (r & 0x13) | ((r & 4) << 1) | ((r & 8) >> 1);
+}
+// Key (or head dim) offset within a 32-row MFMA tile of output element i of a lane in half hf.
+__device__ __forceinline__ constexpr int out_off(int i, int hf) {
+    return (i & 7) + 8 * hf + 16 * (i >> 3);
+}
+
+__device__ __forceinline__ float wave_max_pair(float v) {
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+
+// Output conversion of the o_proj operand (metal/clef.metal:98-106, act16): bf16, or f16
+// that saturates to +-65504 and flags the record when |v| > lim or v is NaN, or plain f32.
+__device__ __forceinline__ void store_out8(void *out, size_t idx, const float *v, int out_type,
+                                           float lim, int32_t *flag) {
+    if (out_type == CLEF_HIP_OUT_BF16) {
+        u32x4 w = {pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
+                   pack_bf16(v[6], v[7])};
+        *(u32x4 *)((uint16_t *)out + idx) = w;
+    } else if (out_type == CLEF_HIP_OUT_F16) {
+        _Float16 h[8];
+        bool bad = false;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float x = v[j];
+            if (!(fabsf(x) <= lim)) {
+                bad = true;
+                x = copysignf(65504.0f, x);
+            }
+            h[j] = (_Float16)x;
+        }
+        if (bad && flag) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *(u32x4 *)((uint16_t *)out + idx) = __builtin_bit_cast(u32x4, h);
+    } else {
+        float *o = (float *)out + idx;
+        *(float4 *)o = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4 *)(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Attention core.
+//   HD   logical head dim (256 text, 72 vision)
+//   HDK  QK^T contraction length, HD rounded up to 16 (also the K / Q plane row stride)
+//   HDM  PV output rows, HD rounded up to 32
+//   BK   keys per LDS tile
+//   TEXT true: Q comes from the fused qkv rows with RMSNorm + rotary applied here and the
+//        sigmoid gate from the same rows; false: Q from a prepared plane, no gate.
+// ------------------------------------------------------------------------------------------
+template <int HD, int BK, bool TEXT>
+struct AttnCfg {
+    static constexpr int HDK = (HD + 15) / 16 * 16;
+    static constexpr int HDM = (HD + 31) / 32 * 32;
+    static constexpr int NC = HDK / 16;          // Q chunks (MFMA k steps of S)
+    static constexpr int NM = HDM / 32;          // O^T row tiles
+    static constexpr int NKT = BK / 32;          // S^T row tiles per key tile
+    static constexpr int KROW = HDK + 8;         // LDS row stride of the K tile (elements)
+    static constexpr int VROW = BK + 8;          // LDS row stride of the V^T tile (elements)
+    static constexpr int KTILE = BK * KROW;
+    static constexpr int VTILE = HDM * VROW;
+    static constexpr int STAGE = KTILE + VTILE;
+    static constexpr int KCHUNKS = BK * HDK / 8;  // 16-byte chunks per K tile
+    static constexpr int VCHUNKS = HD * BK / 8;   // 16-byte chunks per V^T tile (HD rows)
+    static constexpr int KCH = (KCHUNKS + 255) / 256;
+    static constexpr int VCH = (VCHUNKS + 255) / 256;
+};
+
+template <int HD, int BK, bool TEXT>
+__global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
+    using C = AttnCfg<HD, BK, TEXT>;
+    constexpr int HDK = C::HDK, NC = C::NC, NM = C::NM, NKT = C::NKT;
+    constexpr int KROW = C::KROW, VROW = C::VROW;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * C::STAGE];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lq = lane & 31, hf = lane >> 5;
+
+    const int bi = blockIdx.x / p.nh;
+    const int h = blockIdx.x - bi * p.nh;
+    const int32_t *blk = p.blocks + 8 * bi;
+    const int q_row0 = blk[0], nq = blk[1], q_pos0 = blk[2], k_row0 = blk[3], k_len = blk[4];
+    const int flag_row = blk[5];
+    const int kh = h / (p.nh / p.nkv);
+
+    const int my_q = wave * 32 + lq;
+    const bool q_valid = my_q < nq;
+    const int qpos = q_pos0 + my_q;
+    const bool wave_live = wave * 32 < nq;
+    const int wave_last_pos = q_pos0 + wave * 32 + 31;
+
+    // ---- Q prologue: lane holds Q[my_q][c*16 + hf*8 + j] for chunks c, as the S^T B operand.
+    bf16x8 qf[NC];
+    {
+        float x[NC][8];
+        if (TEXT) {
+            const uint16_t *src = p.qkv + (size_t)(q_row0 + (q_valid ? my_q : 0)) * p.row + (size_t)h * 2 * HD;
+            float ss = 0.f;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                u32x4 w = q_valid ? *(const u32x4 *)(src + c * 16 + hf * 8) : u32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    x[c][2 * j] = bf_lo(w[j]);
+                    x[c][2 * j + 1] = bf_hi(w[j]);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) ss += x[c][j] * x[c][j];
+            }
+            ss += __shfl_xor(ss, 32, 64);
+            if (p.q_norm) {   // NULL: no q/k norm (plain SDPA inputs)
+                const float inv = rsqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const float4 w0 = *(const float4 *)(p.q_norm + c * 16 + hf * 8);
+                    const float4 w1 = *(const float4 *)(p.q_norm + c * 16 + hf * 8 + 4);
+                    const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                    for (int j = 0; j < 8; j++) x[c][j] = x[c][j] * inv * wn[j];
+                }
+            }
+            // NeoX partial rotary on the first n_rot dims: pair (i, i + n_rot/2). n_rot/2 is a
+            // multiple of 16, so both dims of a pair sit in the same lane at chunks c, c + R.
+            const int R = p.n_rot / 32;
+            const int32_t *pp = p.pos3 + 3 * (size_t)(q_row0 + (q_valid ? my_q : 0));
+            const float pos3f[3] = {(float)pp[0], (float)pp[1], (float)pp[2]};
+#pragma unroll
+            for (int c = 0; c < NC / 2; c++) {
+                if (c < R) {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const int i = c * 16 + hf * 8 + j;
+                        const float ang = pos3f[i % 3] * p.inv_freq[i];
+                        float sn, cs;
+                        sincosf(ang, &sn, &cs);
+                        const float x0 = x[c][j], x1 = x[c + R][j];
+                        x[c][j] = x0 * cs - x1 * sn;
+                        x[c + R][j] = x1 * cs + x0 * sn;
+                    }
+                }
+            }
+        } else {
+            const uint16_t *src = p.q_plane + ((size_t)h * p.T + q_row0 + (q_valid ? my_q : 0)) * HDK;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                u32x4 w = q_valid ? *(const u32x4 *)(src + c * 16 + hf * 8) : u32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    x[c][2 * j] = bf_lo(w[j]);
+                    x[c][2 * j + 1] = bf_hi(w[j]);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            u32x4 w = {pack_bf16(x[c][0], x[c][1]), pack_bf16(x[c][2], x[c][3]),
+                       pack_bf16(x[c][4], x[c][5]), pack_bf16(x[c][6], x[c][7])};
+            qf[c] = __builtin_bit_cast(bf16x8, w);
+        }
+    }
+
+    // ---- K / V^T tiles: global -> registers -> LDS, double buffered.
+    const uint16_t *kbase = p.k_plane + ((size_t)kh * p.kvT + k_row0) * HDK;
+    const uint16_t *vbase = p.vt_plane + (size_t)kh * HD * p.kvT + k_row0;
+    u32x4 stK[C::KCH], stV[C::VCH];
+
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int j = 0; j < C::KCH; j++) {
+            const int id = tid + 256 * j;
+            const int key = id / (HDK / 8), c8 = id % (HDK / 8);
+            u32x4 w = {0, 0, 0, 0};
+            if ((C::KCHUNKS % 256 == 0 || id < C::KCHUNKS) && kb + key < k_len)
+                w = *(const u32x4 *)(kbase + (size_t)(kb + key) * HDK + c8 * 8);
+            stK[j] = w;
+        }
+#pragma unroll
+        for (int j = 0; j < C::VCH; j++) {
+            const int id = tid + 256 * j;
+            const int d = id / (BK / 8), c8 = id % (BK / 8);
+            const int kk = kb + c8 * 8;
+            u32x4 w = {0, 0, 0, 0};
+            if ((C::VCHUNKS % 256 == 0 || id < C::VCHUNKS) && kk < k_len) {
+                w = *(const u32x4 *)(vbase + (size_t)d * p.kvT + kk);
+                if (kk + 8 > k_len) {   // tail chunk: keys past the record are zero, never stale
+                    const int keep = k_len - kk;   // 1..7 valid bf16 values
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        if (2 * e >= keep) w[e] = 0;
+                        else if (2 * e + 1 >= keep) w[e] &= 0xffffu;
+                    }
+                }
+            }
+            stV[j] = w;
+        }
+    };
+    auto sstore = [&](int buf) {
+        uint16_t *Ks = smem + buf * C::STAGE;
+        uint16_t *Vs = Ks + C::KTILE;
+#pragma unroll
+        for (int j = 0; j < C::KCH; j++) {
+            const int id = tid + 256 * j;
+            if (C::KCHUNKS % 256 == 0 || id < C::KCHUNKS) {
+                const int key = id / (HDK / 8), c8 = id % (HDK / 8);
+                *(u32x4 *)(Ks + key * KROW + c8 * 8) = stK[j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < C::VCH; j++) {
+            const int id = tid + 256 * j;
+            if (C::VCHUNKS % 256 == 0 || id < C::VCHUNKS) {
+                const int d = id / (BK / 8), c8 = id % (BK / 8);
+                *(u32x4 *)(Vs + d * VROW + c8 * 8) = stV[j];
+            }
+        }
+    };
+
+    f32x16 o[NM];
+#pragma unroll
+    for (int mt = 0; mt < NM; mt++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[mt][i] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    const float sl2 = p.scale_log2;
+    const int n_tiles = (k_len + BK - 1) / BK;
+    const int prow = perm_row(lq);
+
+    if (n_tiles > 0) {
+        gload(0);
+        sstore(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < n_tiles; t++) {
+        const int kb = t * BK;
+        const int buf = t & 1;
+        if (t + 1 < n_tiles) gload(kb + BK);
+        const bool active = wave_live && (!p.causal || kb <= wave_last_pos);
+        if (active) {
+            const uint16_t *Ks = smem + buf * C::STAGE;
+            const uint16_t *Vs = Ks + C::KTILE;
+            f32x16 s[NKT];
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) s[kt][i] = 0.f;
+                const uint16_t *kr = Ks + (kt * 32 + prow) * KROW + hf * 8;
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const bf16x8 a = *(const bf16x8 *)(kr + c * 16);
+                    s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c], s[kt], 0, 0, 0);
+                }
+            }
+            // Online softmax in the exp2 domain. Masked scores are -inf, so their P is an
+            // exact zero and a tile past a row's diagonal rescales it by exactly 1.
+            const bool need_mask = (kb + BK > k_len) || (p.causal && kb + BK - 1 > q_pos0 + wave * 32);
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    float v = s[kt][i] * sl2;
+                    if (need_mask) {
+                        const int key = kb + kt * 32 + out_off(i, hf);
+                        if (key >= k_len || (p.causal && key > qpos)) v = -INFINITY;
+                    }
+                    s[kt][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = wave_max_pair(mx);
+            const float mn = fmaxf(m_run, mx);
+            const float msub = (mn == -INFINITY) ? 0.f : mn;
+            const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
+            float rs = 0.f;
+            bf16x8 pk[NKT][2];
+#pragma unroll
+            for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                for (int cc = 0; cc < 2; cc++) {
+                    unsigned w[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float p0 = __builtin_amdgcn_exp2f(s[kt][cc * 8 + 2 * j] - msub);
+                        const float p1 = __builtin_amdgcn_exp2f(s[kt][cc * 8 + 2 * j + 1] - msub);
+                        w[j] = pack_bf16(p0, p1);
+                        // The row sum takes the rounded P that the PV product multiplies.
+                        rs += bf_lo(w[j]) + bf_hi(w[j]);
+                    }
+                    u32x4 wv = {w[0], w[1], w[2], w[3]};
+                    pk[kt][cc] = __builtin_bit_cast(bf16x8, wv);
+                }
+            rs += __shfl_xor(rs, 32, 64);
+            l_run = l_run * alpha + rs;
+            m_run = mn;
+            if (__any(alpha != 1.f)) {
+#pragma unroll
+                for (int mt = 0; mt < NM; mt++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) o[mt][i] *= alpha;
+            }
+#pragma unroll
+            for (int mt = 0; mt < NM; mt++) {
+                const uint16_t *vr = Vs + (mt * 32 + prow) * VROW + hf * 8;
+#pragma unroll
+                for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                    for (int cc = 0; cc < 2; cc++) {
+                        const bf16x8 a = *(const bf16x8 *)(vr + kt * 32 + cc * 16);
+                        o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[kt][cc], o[mt], 0, 0, 0);
+                    }
+            }
+        }
+        if (t + 1 < n_tiles) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- Epilogue: O / l, times sigmoid(gate) for text, converted and stored.
+    if (q_valid) {
+        const float il = l_run > 0.f ? 1.f / l_run : 0.f;
+        const size_t t = (size_t)q_row0 + my_q;
+        int32_t *flag = p.ovf ? p.ovf + flag_row : nullptr;
+#pragma unroll
+        for (int mt = 0; mt < NM; mt++)
+#pragma unroll
+            for (int run = 0; run < 2; run++) {
+                const int d0 = mt * 32 + 16 * run + 8 * hf;
+                if (d0 >= HD) continue;
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = o[mt][run * 8 + j] * il;
+                if (TEXT && p.gate) {
+                    const u32x4 g = *(const u32x4 *)(p.qkv + t * p.row + (size_t)h * 2 * HD + HD + d0);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        v[2 * j] *= 1.f / (1.f + expf(-bf_lo(g[j])));
+                        v[2 * j + 1] *= 1.f / (1.f + expf(-bf_hi(g[j])));
+                    }
+                }
+                store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);
+            }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Text K/V prologue (metal/clef.metal:245-300 and 873-928 for K and V): per kv row of the
+// plan, K = RMSNorm(k) * (1+w) then partial rotary, written to the K plane [nkv][kvT][HD];
+// V copied unnormalised and written transposed to the V^T plane [nkv][HD][kvT]. Rows whose
+// kv_tok is negative (cached prefix rows, alignment padding) are left untouched.
+// Grid (kv_rows / 64, nkv), 256 threads; each wave handles 16 rows, a lane 4 dims.
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void text_prep_kv_kernel(PrepParams p) {
+    constexpr int HD = 256, ROWS = 64;
+    __shared__ __attribute__((aligned(16))) uint16_t vt[HD * (ROWS + 8)];
+    __shared__ int toks[ROWS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int row0 = blockIdx.x * ROWS, kh = blockIdx.y;
+    if (tid < ROWS) toks[tid] = (row0 + tid < p.kv_rows) ? p.kv_tok[row0 + tid] : -1;
+    __syncthreads();
+    const int half_rot = p.n_rot / 2;
+    for (int r = wave * 16; r < wave * 16 + 16; r++) {
+        const int tok = toks[r];
+        if (tok < 0) continue;
+        const uint16_t *src = p.qkv + (size_t)tok * p.row + (size_t)p.nh * 2 * HD + (size_t)kh * HD;
+        const u32x2 w = *(const u32x2 *)(src + 4 * lane);
+        float x[4] = {bf_lo(w[0]), bf_hi(w[0]), bf_lo(w[1]), bf_hi(w[1])};
+        float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off, 64);
+        if (p.k_norm) {
+            const float inv = rsqrtf(ss / (float)HD + p.eps);
+            const float4 wn = *(const float4 *)(p.k_norm + 4 * lane);
+            x[0] *= inv * wn.x; x[1] *= inv * wn.y; x[2] *= inv * wn.z; x[3] *= inv * wn.w;
+        }
+        // Rotary pair (i, i + half_rot): lanes own 4 consecutive dims, so the partner of lane
+        // L's dims sits in lane L ^ (half_rot / 4) (half_rot is a power of two >= 4 here).
+        const int xo = half_rot / 4;
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) y[e] = __shfl_xor(x[e], xo > 0 ? xo : 1, 64);
+        if (4 * lane < p.n_rot) {
+            const bool first = (4 * lane) < half_rot;
+            const int32_t *pp = p.pos3 + 3 * (size_t)tok;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int i = (4 * lane + e) % half_rot;
+                const float ang = (float)pp[i % 3] * p.inv_freq[i];
+                float sn, cs;
+                sincosf(ang, &sn, &cs);
+                x[e] = first ? x[e] * cs - y[e] * sn : x[e] * cs + y[e] * sn;
+            }
+        }
+        const int kvr = row0 + r;
+        u32x2 ko = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])};
+        *(u32x2 *)(p.k_plane + ((size_t)kh * p.kvT + kvr) * HD + 4 * lane) = ko;
+        const uint16_t *vs = src + (size_t)p.nkv * HD;
+        const u32x2 vw = *(const u32x2 *)(vs + 4 * lane);
+        vt[(4 * lane + 0) * (ROWS + 8) + r] = (uint16_t)(vw[0] & 0xffff);
+        vt[(4 * lane + 1) * (ROWS + 8) + r] = (uint16_t)(vw[0] >> 16);
+        vt[(4 * lane + 2) * (ROWS + 8) + r] = (uint16_t)(vw[1] & 0xffff);
+        vt[(4 * lane + 3) * (ROWS + 8) + r] = (uint16_t)(vw[1] >> 16);
+    }
+    __syncthreads();
+    // V^T rows: HD dims x 64 keys, 16-byte chunks of 8 keys.
+    for (int id = tid; id < HD * (ROWS / 8); id += 256) {
+        const int d = id / (ROWS / 8), c8 = id % (ROWS / 8);
+        uint16_t *dst = p.vt_plane + ((size_t)kh * HD + d) * p.kvT + row0 + c8 * 8;
+        bool all = true;
+#pragma unroll
+        for (int e = 0; e < 8; e++) all = all && toks[c8 * 8 + e] >= 0;
+        if (all) {
+            *(u32x4 *)dst = *(const u32x4 *)(vt + d * (ROWS + 8) + c8 * 8);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (toks[c8 * 8 + e] >= 0) dst[e] = vt[d * (ROWS + 8) + c8 * 8 + e];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Vision prologue (metal/clef.metal:1616-1656, vis_qkv_rope): qkv [P][3E] (+ bias) ->
+// Q plane [heads][P][VHDK], K plane [heads][kvT][VHDK] (rows kv_row), V^T [heads][VHD][kvT].
+// Q and K take the 2-D rotary: pair (i, i + hd/2); the first hd/4 pairs turn by the patch's
+// grid row, the rest by its column. pos2 [P][2] holds each patch's (row, column).
+// Grid (kv_rows / 64, heads), 256 threads; lane i < hd/2 of a wave owns dims i and i + hd/2.
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void vis_prep_kernel(VisPrepParams p) {
+    constexpr int HD = 72, HDK = 80, ROWS = 64, HALF = HD / 2, QUART = HD / 4;
+    __shared__ __attribute__((aligned(16))) uint16_t vt[HD * (ROWS + 8)];
+    __shared__ int toks[ROWS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int row0 = blockIdx.x * ROWS, h = blockIdx.y;
+    const int E = p.heads * HD;
+    if (tid < ROWS) toks[tid] = (row0 + tid < p.kv_rows) ? p.kv_tok[row0 + tid] : -1;
+    __syncthreads();
+    for (int r = wave * 16; r < wave * 16 + 16; r++) {
+        const int tok = toks[r];
+        if (tok < 0) continue;
+        const int kvr = row0 + r;
+        const uint16_t *row = p.qkv + (size_t)tok * 3 * E;
+        if (lane < HALF) {
+            const int i = lane;
+            const float ang = (float)p.pos2[2 * tok + (i < QUART ? 0 : 1)] * p.inv_freq[i < QUART ? i : i - QUART];
+            float sn, cs;
+            sincosf(ang, &sn, &cs);
+#pragma unroll
+            for (int part = 0; part < 2; part++) {
+                const int base = part * E + h * HD;
+                float x0 = bf2f(row[base + i]), x1 = bf2f(row[base + i + HALF]);
+                if (p.bias) { x0 += p.bias[base + i]; x1 += p.bias[base + i + HALF]; }
+                const float y0 = x0 * cs - x1 * sn, y1 = x1 * cs + x0 * sn;
+                uint16_t *dst = part == 0 ? p.q_plane + ((size_t)h * p.P + tok) * HDK
+                                          : p.k_plane + ((size_t)h * p.kvT + kvr) * HDK;
+                dst[i] = f2bf(y0);
+                dst[i + HALF] = f2bf(y1);
+            }
+            const int vb = 2 * E + h * HD;
+            float v0 = bf2f(row[vb + i]), v1 = bf2f(row[vb + i + HALF]);
+            if (p.bias) { v0 += p.bias[vb + i]; v1 += p.bias[vb + i + HALF]; }
+            vt[i * (ROWS + 8) + r] = f2bf(v0);
+            vt[(i + HALF) * (ROWS + 8) + r] = f2bf(v1);
+        } else if (lane < HALF + (HDK - HD)) {
+            // zero the contraction padding dims of Q and K
+            const int d = HD + (lane - HALF);
+            p.q_plane[((size_t)h * p.P + tok) * HDK + d] = 0;
+            p.k_plane[((size_t)h * p.kvT + kvr) * HDK + d] = 0;
+        }
+    }
+    __syncthreads();
+    for (int id = tid; id < HD * (ROWS / 8); id += 256) {
+        const int d = id / (ROWS / 8), c8 = id % (ROWS / 8);
+        uint16_t *dst = p.vt_plane + ((size_t)h * HD + d) * p.kvT + row0 + c8 * 8;
+        bool all = true;
+#pragma unroll
+        for (int e = 0; e < 8; e++) all = all && toks[c8 * 8 + e] >= 0;
+        if (all) {
+            *(u32x4 *)dst = *(const u32x4 *)(vt + d * (ROWS + 8) + c8 * 8);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (toks[c8 * 8 + e] >= 0) dst[e] = vt[d * (ROWS + 8) + c8 * 8 + e];
+        }
+    }
+}
+
+}  // namespace clef_hip

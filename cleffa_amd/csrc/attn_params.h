@@ -1,0 +1,49 @@
+// Kernel argument blocks shared by the HIP kernels and the host layer (internal).
+#pragma once
+#include <stdint.h>
+
+#include "clef_hip_attn.h"
+
+namespace clef_hip {
+
+struct AttnParams {
+    const uint16_t *qkv;      // text: fused qkv rows [T][row]
+    const float *q_norm;
+    const int32_t *pos3;
+    const float *inv_freq;
+    const uint16_t *q_plane;  // vision: prepared Q [heads][T][HDK]
+    const uint16_t *k_plane;
+    const uint16_t *vt_plane;
+    const int32_t *blocks;
+    void *out;
+    int32_t *ovf;
+    int row, T, kvT, nh, nkv, n_rot;
+    float eps, scale_log2, f16_lim;
+    int causal, gate, out_type, out_ld;
+};
+
+struct PrepParams {
+    const uint16_t *qkv;
+    const float *k_norm;
+    const int32_t *pos3;
+    const float *inv_freq;
+    const int32_t *kv_tok;
+    uint16_t *k_plane;
+    uint16_t *vt_plane;
+    int row, nh, nkv, n_rot, kvT, kv_rows;
+    float eps;
+};
+
+struct VisPrepParams {
+    const uint16_t *qkv;
+    const float *bias;
+    const int32_t *pos2;
+    const float *inv_freq;
+    const int32_t *kv_tok;
+    uint16_t *q_plane;
+    uint16_t *k_plane;
+    uint16_t *vt_plane;
+    int P, heads, kvT, kv_rows;
+};
+
+}  // namespace clef_hip

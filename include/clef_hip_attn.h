@@ -1,0 +1,147 @@
+/* clef_hip_attn.h - C ABI of the MI355X (gfx950) prefill attention path for cleffa.
+ *
+ * This library replaces the attention dispatch inside cleffa's GPU backend. The engine's public
+ * entry points clef_gpu_forward and clef_gpu_forward_prefix (clef_engine.h:178-205) keep their
+ * signatures; inside them the full-attention layer calls clef_hip_attn_prefill where the Metal
+ * backend calls encode_attention_tu (clef_metal.m:829-882) or its FP32 branch
+ * (clef_metal.m:1330-1413), and the vision tower calls clef_hip_vis_attention where it runs
+ * vis_qkv_rope + vis_attention_mma/_mpp (clef_metal.m:1022-1049).
+ *
+ * Conventions (clef_metal.m:83-86, 39-49): every entry point returns true on success; on failure
+ * it returns false and writes a message starting with "hip: " into err (errlen bytes, may be
+ * NULL/0) and launches nothing further. Device pointers are plain pointers into device memory;
+ * `stream` is a hipStream_t passed as void * (NULL = the default stream). Calls are asynchronous
+ * with respect to the host and not reentrant for buffers they share. Nothing here allocates
+ * device memory: the caller owns every buffer (clef_metal.m:337-412 ownership model).
+ *
+ * Layouts (bf16 = raw uint16 bits):
+ *   qkv     [T][row] bf16, the fused projection row: [nh x (query hd | gate hd)] [nkv x hd K]
+ *           [nkv x hd V] (tools/convert.py:23-25, metal/clef.metal:245-248).
+ *   pos3    [T][3] int32 rotary positions per pass row (temporal, grid row, grid column).
+ *   K plane [nkv][kvT][hd] bf16, normalised and rotated keys, one row per key.
+ *   V^T     [nkv][hd][kvT] bf16, values transposed (keys contiguous per head dim).
+ *   out     [T][nh*hd] (text) or [P][heads*hd] (vision): the o_proj operand, bf16 / f16 / f32.
+ *   The plan (clef_hip_attn_plan) maps records to query blocks and kv rows; it is built once per
+ *   pass on the host and copied to the device, then reused by every attention layer of the pass,
+ *   as the Metal backend builds attn_blk once per forward (clef_metal.m:1243-1257).
+ */
+#ifndef CLEF_HIP_ATTN_H
+#define CLEF_HIP_ATTN_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CLEF_HIP_OUT_BF16 0 /* bf16 (act16 with f16 off, metal/clef.metal:101) */
+#define CLEF_HIP_OUT_F16 1  /* f16; |v| > f16_lim or NaN saturates and flags (metal/clef.metal:98-106) */
+#define CLEF_HIP_OUT_F32 2  /* f32 (CLEF_VIS_F32 / FP32 kernels' unrounded output) */
+
+#define CLEF_HIP_BLOCK_Q 128  /* query rows per block */
+#define CLEF_HIP_KV_ALIGN 64  /* kv row alignment of each record in a fresh pass */
+#define CLEF_HIP_BLOCK_INTS 8 /* int32 per block entry */
+
+/* Library version and the wave size the kernels were compiled for (64). The Metal backend
+ * refuses attention pipelines that are not 32 lanes wide (clef_metal.m:95-108); this is the
+ * CDNA equivalent: clef_hip_attn_init fails unless the device runs 64-wide wavefronts. */
+int clef_hip_attn_version(void);
+int clef_hip_attn_wave_size(void);
+
+/* Checks the current device (gfx950, wave64, LDS for the kernels) and sets kernel attributes.
+ * Call once per device before the first launch. Replaces the pipeline checks of clef_gpu_open
+ * (clef_metal.m:95-108, 133-140). */
+bool clef_hip_attn_init(char *err, size_t errlen);
+
+/* Upper bounds for the plan arrays of a pass with n_seq records and Tq query / Tk key rows. */
+int clef_hip_attn_plan_max_blocks(int n_seq, int Tq);
+int clef_hip_attn_plan_max_kv_rows(int n_seq, int Tk);
+
+/* Host-only: builds the query-block list and the kv-row map of a pass (clef_metal.m:1243-1257
+ * block list; clef.c:470-497 packing). cu_q[n_seq+1] are the records' pass-row bounds
+ * (seq_bounds). cu_k = NULL is a fresh pass: every record's keys are its own queries and the
+ * plan lays them out at 64-aligned kv rows. cu_k != NULL is a prefix-cache pass
+ * (clef_gpu_forward_prefix, clef_metal.m:1640-1666): record r's keys occupy kv rows
+ * cu_k[r] .. cu_k[r+1] (multiples of 8), its first cu_k[r+1]-cu_k[r]-(cu_q[r+1]-cu_q[r]) keys are
+ * cached, and its queries are the last tokens. causal = 0 gives bidirectional attention within
+ * each record (vision). Outputs: blocks [max_blocks][8] (sorted longest first), kv_tok [max_kv]
+ * (pass row whose K/V lands in that kv row, or -1), *n_blk, *kv_rows (rows per head the K and
+ * V^T planes need; a multiple of 64). */
+bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int causal,
+                        int32_t *blocks, int max_blocks, int32_t *kv_tok, int max_kv,
+                        int *n_blk, int *kv_rows, char *err, size_t errlen);
+
+/* RoPE frequency table: inv_freq[j] = 1 / theta^(2j/n_rot) in f32, j < n_rot/2
+ * (clef_metal.m:176-184 text, 186-192 vision with n_rot = hd/2 and theta = 10000). */
+void clef_hip_rope_inv_freq(float theta, int n_rot, float *inv_freq);
+
+/* Host-only: per-patch (grid row, grid column) of the vision rotary, patches stored in
+ * merge x merge window order (metal/clef.metal:1639-1641). pos2 [cu[n_img]][2]. */
+bool clef_hip_vis_positions(const int32_t *cu, int n_img, const int32_t *grid_w, int merge,
+                            int32_t *pos2, char *err, size_t errlen);
+
+/* One full-attention layer of the dense text models (hd 256, GQA). */
+typedef struct {
+    int nh, nkv, hd, n_rot;   /* hd must be 256; n_rot in {0, 32, 64, 128, 256} */
+    float eps, scale;         /* RMSNorm eps (1e-6), softmax scale (1/sqrt(hd)) */
+    int T, row;               /* pass rows; qkv row stride in elements (multiple of 8) */
+    const uint16_t *qkv;      /* [T][row] bf16 */
+    const float *q_norm;      /* [hd] f32, already 1 + w (tools/convert.py:7-8); NULL with k_norm: no norm */
+    const float *k_norm;      /* [hd] f32, already 1 + w */
+    const int32_t *pos3;      /* [T][3] */
+    const float *inv_freq;    /* [n_rot/2] */
+    uint16_t *k_plane;        /* [nkv][kvT][hd] */
+    uint16_t *vt_plane;       /* [nkv][hd][kvT] */
+    int kvT;                  /* rows per head of the planes: >= plan kv_rows, multiple of 8 */
+    const int32_t *blocks;    /* device copy of the plan's blocks */
+    int n_blk;
+    const int32_t *kv_tok;    /* device copy of the plan's kv_tok */
+    int kv_rows;
+    int causal;               /* 1 for the text models */
+    int gate;                 /* 1: multiply by sigmoid(gate) (Qwen3.5 gated attention) */
+    void *out;                /* [T][nh*hd] */
+    int out_type;             /* CLEF_HIP_OUT_* */
+    float f16_lim;            /* overflow limit for CLEF_HIP_OUT_F16 (65504) */
+    int32_t *ovf;             /* [T] int32 flags, set at the record's first pass row; may be NULL */
+} clef_hip_attn_args;
+
+/* K/V prologue only: RMSNorm + rotary of K into the K plane, V into the V^T plane, for every
+ * kv row whose kv_tok >= 0 (attn_prep / attn_prep_split / attn_prep_prefix K and V parts,
+ * metal/clef.metal:245-300, 657-707, 873-928). */
+bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen);
+/* Attention core with the Q prologue and gate epilogue fused (attention_tu and the FP32
+ * kernels, metal/clef.metal:316-654, 709-849, 930-1093). Reads the planes prep_kv wrote. */
+bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen);
+/* prep_kv then core: the whole attention step of one layer (encode_attention_tu). */
+bool clef_hip_attn_prefill(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen);
+
+/* Vision tower attention (hd 72, MHA, bidirectional within each image). */
+typedef struct {
+    int P, heads, hd;         /* hd must be 72 */
+    float scale;              /* 1/sqrt(hd) */
+    const uint16_t *qkv;      /* [P][3*heads*hd] bf16 */
+    const float *bias;        /* [3*heads*hd] f32 or NULL */
+    const int32_t *pos2;      /* [P][2] grid (row, column) per patch */
+    const float *inv_freq;    /* [hd/4] */
+    uint16_t *q_plane;        /* [heads][P][80] scratch */
+    uint16_t *k_plane;        /* [heads][kvT][80] scratch */
+    uint16_t *vt_plane;       /* [heads][hd][kvT] scratch */
+    int kvT;
+    const int32_t *blocks;
+    int n_blk;
+    const int32_t *kv_tok;
+    int kv_rows;
+    void *out;                /* [P][heads*hd] */
+    int out_type;
+    float f16_lim;
+    int32_t *ovf;             /* [P] or NULL; flag at the image's first patch */
+} clef_hip_vis_args;
+
+bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
