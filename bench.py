@@ -1,0 +1,192 @@
+"""Benchmark of the prefill attention hot path on one MI355X.
+
+One step = one full-attention layer over the C1 micro-batch (8 packed causal records, 4,096
+tokens, 24/4 heads, hd 256): the K/V prologue kernel plus the attention kernel with the fused
+Q prologue and gate epilogue, on inputs already resident in HBM. Steps are replayed from a HIP
+graph (captured once) so host launch cost is not part of the GPU time; the timed region is
+bracketed by torch.cuda.synchronize() and HIP events on the launch stream.
+
+Prints one JSON line. `value` is algorithmic TFLOP/s of the whole step (QK^T + PV flops,
+4*hd*nh*pairs); `roofline` covers the attention kernel alone, timed the same way;
+`cpu_baseline` is the fp32 CPU oracle (OpenMP) on the same C1 inputs.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (published)
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3", "C4"])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
+    return ap.parse_args()
+
+
+def build_step(cfg, seed):
+    """Returns (step_fn, core_fn, info) for one configuration, inputs resident on cuda:0."""
+    from cleffa_amd import AttnPlan, TextAttention, VisionAttention, workloads
+    dev = torch.device("cuda", 0)
+    w = workloads.config(cfg, seed=seed, device=dev)
+    if cfg == "C4":
+        vis = VisionAttention(w["heads"], w["hd"], device=dev)
+        plan = AttnPlan(w["cu_seqlens"], causal=False, device=dev)
+        out = torch.empty((plan.T, vis.E), dtype=torch.bfloat16, device=dev)
+        scratch = vis.scratch(plan.T, plan.kvT)
+        step = lambda: vis.forward(w["qkv"], w["bias"], w["pos2"], plan, out=out, scratch=scratch)
+        info = dict(workload="C4 vision: 4 images x 1,024 patches (32x32), bidirectional, 16 heads MHA, "
+                    "hd 72, 2-D rotary", tokens=plan.T, pairs=plan.pairs(), hd=w["hd"], nh=w["heads"],
+                    bytes=plan.T * 3 * vis.E * 2 + plan.T * vis.E * 2, core=None)
+        return step, None, info, w
+    att = TextAttention(w["nh"], w["nkv"], w["hd"], w["n_rot"], rope_theta=w["theta"], device=dev)
+    if cfg == "C3":
+        plan = AttnPlan(w["cu_seqlens"], w["cu_seqlens_k"], causal=True, device=dev)
+        kp = w["k_cache"].contiguous()
+        vt = w["v_cache"].transpose(1, 2).contiguous()
+        kvT = kp.shape[1]
+    else:
+        plan = AttnPlan(w["cu_seqlens"], causal=True, device=dev)
+        kvT = plan.kvT
+        kp, vt = att.planes(kvT)
+    out = torch.empty((plan.T, w["nh"] * w["hd"]), dtype=torch.bfloat16, device=dev)
+    kwargs = dict(out=out, gate=w["gate"], k_plane=kp, vt_plane=vt, kvT=kvT)
+    args = (w["qkv"], w["q_norm"], w["k_norm"], w["pos3"], plan)
+    step = lambda: att.forward(*args, stage="prefill", **kwargs)
+    core = lambda: att.forward(*args, stage="core", **kwargs)
+    T, nh, nkv, hd = plan.T, w["nh"], w["nkv"], w["hd"]
+    # algorithmic bytes: qkv rows read once, O written once, cached K/V read (C3)
+    nbytes = T * (2 * nh + 2 * nkv) * hd * 2 + T * nh * hd * 2
+    if cfg == "C3":
+        nbytes += 2 * nkv * (int(w["cu_seqlens_k"][-1]) - T) * hd * 2
+    names = {"C1": "C1 packed varlen causal micro-batch: 8 records, 4,096 tokens, 24/4 heads, hd 256, "
+                   "fused q/k RMSNorm + rotary(64, theta 1e7) + sigmoid gate",
+             "C2": "C2 single causal request: 16,384 tokens, 24/4 heads, hd 256, fused prologue/gate",
+             "C3": "C3 prefix-cache continuation: 4 x (2,048 cached + 512 new), 16/4 heads, hd 256"}
+    info = dict(workload=names[cfg], tokens=T, pairs=plan.pairs(), hd=hd, nh=nh, bytes=nbytes,
+                lengths=[int(x) for x in np.diff(plan.cu_q)])
+    return step, core, info, w
+
+
+def time_fn(fn, steps, warmup, graph):
+    """Mean ms per call over `steps` calls (HIP events on the launch stream)."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    per = 1
+    g = None
+    if graph:
+        per = next(d for d in (10, 5, 4, 2, 1) if steps % d == 0)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(per):
+                fn()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    if g is not None:
+        for _ in range(steps // per):
+            g.replay()
+    else:
+        for _ in range(steps):
+            fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    return start.elapsed_time(end) / steps, wall / steps
+
+
+def cpu_baseline(w, cfg):
+    """fp32 CPU oracle (OpenMP) on the same inputs: prologue + attention, median of 5 runs."""
+    from cleffa_amd import rope_inv_freq
+    from oracle import oracle
+    qkv = w["qkv"].float().cpu().numpy()
+    nh, nkv, hd, n_rot = w["nh"], w["nkv"], w["hd"], w["n_rot"]
+    inv = rope_inv_freq(w["theta"], n_rot)
+    qn, kn, pos = w["q_norm"].cpu().numpy(), w["k_norm"].cpu().numpy(), w["pos3"].cpu().numpy()
+
+    def run():
+        Q, K, V, G = oracle.text_prep(qkv, nh, nkv, hd, n_rot, qn, kn, pos, inv, precision="f32")
+        oracle.attention(Q, K, V, w["cu_seqlens"], None, True, hd ** -0.5, G, precision="f32")
+
+    run()
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), oracle.num_threads()
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                          "(sharding is described in DESIGN.md, not launched)"}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(2)
+    torch.cuda.set_device(0)
+    step, core, info, w = build_step(a.config, a.seed)
+    graph = not a.no_graph
+    ms, wall_ms = time_fn(step, a.steps, a.warmup, graph)
+    flops = 4.0 * info["hd"] * info["nh"] * info["pairs"]
+    tflops = flops / (ms * 1e-3) / 1e12
+    res = {
+        "metric": "prefill attention TFLOP/s (4096-tok packed causal GQA micro-batch, hd 256)"
+        if a.config == "C1" else f"prefill attention TFLOP/s ({a.config})",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "tokens_per_s": round(info["tokens"] / (ms * 1e-3), 1),
+        "mfma_peak_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 5), "host_ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs, random-init norm weights)",
+        "config": {"workload": info["workload"], "seed": a.seed, "tokens": info["tokens"],
+                   "pairs": info["pairs"], "gflop": round(flops / 1e9, 3),
+                   **({"lengths": info["lengths"]} if "lengths" in info else {})},
+    }
+    if core is not None:
+        core_ms, _ = time_fn(core, a.steps, a.warmup, graph)
+        achieved = flops / (core_ms * 1e-3) / 1e12
+        res["roofline"] = {"bound": "mfma", "kernel": "attn_fwd_kernel<256,64,true>",
+                           "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                           "launch_ms": round(core_ms, 5),
+                           "algorithmic_bytes": info["bytes"],
+                           "hbm_frac_at_this_time": round(info["bytes"] / (core_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        res["prep_ms"] = round(ms - core_ms, 5)
+    if not a.no_cpu and a.config in ("C1", "C2") and a.config == "C1":
+        sec, threads = cpu_baseline(w, a.config)
+        res["cpu_baseline"] = {"value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s",
+                               "tokens_per_s": round(info["tokens"] / sec, 1), "ms": round(sec * 1e3, 2),
+                               "cores": threads, "kind": "port",
+                               "sample": "the full C1 step (prologue + attention, 4,096 tokens) in fp32, "
+                                         "median of 5 runs"}
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -42,7 +42,8 @@ bool launch_ok(const char *what, char *err, size_t errlen) {
 }
 
 bool rot_ok(int n_rot, int hd) {
-    return (n_rot == 0 || n_rot == 32 || n_rot == 64 || n_rot == 128 || n_rot == 256) && n_rot <= hd;
+    // the fused Q prologue is compiled for these rotary widths (Clef pins 64, clef.c:116-120)
+    return (n_rot == 0 || n_rot == 64) && n_rot <= hd;
 }
 
 bool check_text(const clef_hip_attn_args *a, bool need_core, char *err, size_t errlen) {
@@ -206,7 +207,10 @@ bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, si
     p.out_ld = a->nh * a->hd;
     const long grid = (long)a->n_blk * a->nh;
     if (grid > 0x7fffffffL) return fail(err, errlen, "grid too large");
-    hipLaunchKernelGGL((attn_fwd_kernel<256, 64, true>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+    if (a->n_rot == 64)
+        hipLaunchKernelGGL((attn_fwd_kernel<256, 64, true, 64, true>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+    else
+        hipLaunchKernelGGL((attn_fwd_kernel<256, 64, true, 0, true>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
     return launch_ok("attn_fwd<256>", err, errlen);
 }
 
@@ -244,7 +248,7 @@ bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err,
     p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = a->f16_lim;
     p.causal = 0; p.gate = 0; p.out_type = a->out_type; p.out_ld = a->heads * kVisHD;
     (void)kVisHDK;
-    hipLaunchKernelGGL((attn_fwd_kernel<72, 64, false>), dim3((unsigned)(a->n_blk * a->heads)), dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((attn_fwd_kernel<72, 64, false, 0, false>), dim3((unsigned)(a->n_blk * a->heads)), dim3(256), 0, (hipStream_t)stream, p);
     return launch_ok("attn_fwd<72>", err, errlen);
 }
 

@@ -89,22 +89,26 @@ __device__ __forceinline__ void store_out8(void *out, size_t idx, const float *v
 
 // ------------------------------------------------------------------------------------------
 // Attention core.
-//   HD   logical head dim (256 text, 72 vision)
-//   HDK  QK^T contraction length, HD rounded up to 16 (also the K / Q plane row stride)
-//   HDM  PV output rows, HD rounded up to 32
-//   BK   keys per LDS tile
-//   TEXT true: Q comes from the fused qkv rows with RMSNorm + rotary applied here and the
-//        sigmoid gate from the same rows; false: Q from a prepared plane, no gate.
+//   HD     logical head dim (256 text, 72 vision)
+//   HDK    QK^T contraction length, HD rounded up to 16 (also the K / Q plane row stride)
+//   HDM    PV output rows, HD rounded up to 32
+//   BK     keys per LDS tile (64)
+//   TEXT   true: Q comes from the fused qkv rows with RMSNorm + rotary applied here and the
+//          sigmoid gate from the same rows; false: Q from a prepared plane, no gate.
+//   NROT   rotary dims of the text Q prologue (0 or a multiple of 32)
+//   DIRECT true: K / V^T tiles go global -> LDS with global_load_lds (no VGPR staging) into
+//          unpadded, XOR-swizzled LDS rows; needs 512-byte K rows (HD 256). false: tiles are
+//          staged through VGPRs into padded LDS rows.
 // ------------------------------------------------------------------------------------------
-template <int HD, int BK, bool TEXT>
+template <int HD, int BK, bool DIRECT>
 struct AttnCfg {
     static constexpr int HDK = (HD + 15) / 16 * 16;
     static constexpr int HDM = (HD + 31) / 32 * 32;
     static constexpr int NC = HDK / 16;          // Q chunks (MFMA k steps of S)
     static constexpr int NM = HDM / 32;          // O^T row tiles
     static constexpr int NKT = BK / 32;          // S^T row tiles per key tile
-    static constexpr int KROW = HDK + 8;         // LDS row stride of the K tile (elements)
-    static constexpr int VROW = BK + 8;          // LDS row stride of the V^T tile (elements)
+    static constexpr int KROW = DIRECT ? HDK : HDK + 8;   // LDS row stride of the K tile (elements)
+    static constexpr int VROW = DIRECT ? BK : BK + 8;     // LDS row stride of the V^T tile (elements)
     static constexpr int KTILE = BK * KROW;
     static constexpr int VTILE = HDM * VROW;
     static constexpr int STAGE = KTILE + VTILE;
@@ -112,13 +116,17 @@ struct AttnCfg {
     static constexpr int VCHUNKS = HD * BK / 8;   // 16-byte chunks per V^T tile (HD rows)
     static constexpr int KCH = (KCHUNKS + 255) / 256;
     static constexpr int VCH = (VCHUNKS + 255) / 256;
+    static_assert(!DIRECT || (HDK == 256 && BK == 64 && HD == HDM), "direct tiles assume hd 256, 64 keys");
 };
 
-template <int HD, int BK, bool TEXT>
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int HD, int BK, bool TEXT, int NROT, bool DIRECT>
 __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
-    using C = AttnCfg<HD, BK, TEXT>;
+    using C = AttnCfg<HD, BK, DIRECT>;
     constexpr int HDK = C::HDK, NC = C::NC, NM = C::NM, NKT = C::NKT;
     constexpr int KROW = C::KROW, VROW = C::VROW;
+    static_assert(NROT % 32 == 0 && NROT <= HDK, "rotary dims");
     __shared__ __attribute__((aligned(16))) uint16_t smem[2 * C::STAGE];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -141,8 +149,9 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
     bf16x8 qf[NC];
     {
         float x[NC][8];
+        const size_t qrow = (size_t)q_row0 + (q_valid ? my_q : 0);
         if (TEXT) {
-            const uint16_t *src = p.qkv + (size_t)(q_row0 + (q_valid ? my_q : 0)) * p.row + (size_t)h * 2 * HD;
+            const uint16_t *src = p.qkv + qrow * p.row + (size_t)h * 2 * HD;
             float ss = 0.f;
 #pragma unroll
             for (int c = 0; c < NC; c++) {
@@ -167,20 +176,24 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
                     for (int j = 0; j < 8; j++) x[c][j] = x[c][j] * inv * wn[j];
                 }
             }
-            // NeoX partial rotary on the first n_rot dims: pair (i, i + n_rot/2). n_rot/2 is a
-            // multiple of 16, so both dims of a pair sit in the same lane at chunks c, c + R.
-            const int R = p.n_rot / 32;
-            const int32_t *pp = p.pos3 + 3 * (size_t)(q_row0 + (q_valid ? my_q : 0));
-            const float pos3f[3] = {(float)pp[0], (float)pp[1], (float)pp[2]};
+            if (NROT > 0) {
+                // NeoX partial rotary: pair (i, i + NROT/2), both dims in this lane at chunks
+                // c and c + R. Interleaved M-RoPE: pair i turns by axis i % 3 of pos3.
+                constexpr int R = NROT / 32;
+                const int32_t *pp = p.pos3 + 3 * qrow;
+                const float pt = (float)pp[0], ph = (float)pp[1], pw = (float)pp[2];
 #pragma unroll
-            for (int c = 0; c < NC / 2; c++) {
-                if (c < R) {
+                for (int c = 0; c < R; c++) {
+                    const float4 f0 = *(const float4 *)(p.inv_freq + c * 16 + hf * 8);
+                    const float4 f1 = *(const float4 *)(p.inv_freq + c * 16 + hf * 8 + 4);
+                    const float fr[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
                         const int i = c * 16 + hf * 8 + j;
-                        const float ang = pos3f[i % 3] * p.inv_freq[i];
+                        const int ax = i % 3;
+                        const float pos = ax == 0 ? pt : (ax == 1 ? ph : pw);
                         float sn, cs;
-                        sincosf(ang, &sn, &cs);
+                        sincosf(pos * fr[j], &sn, &cs);
                         const float x0 = x[c][j], x1 = x[c + R][j];
                         x[c][j] = x0 * cs - x1 * sn;
                         x[c + R][j] = x1 * cs + x0 * sn;
@@ -188,7 +201,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
                 }
             }
         } else {
-            const uint16_t *src = p.q_plane + ((size_t)h * p.T + q_row0 + (q_valid ? my_q : 0)) * HDK;
+            const uint16_t *src = p.q_plane + ((size_t)h * p.T + qrow) * HDK;
 #pragma unroll
             for (int c = 0; c < NC; c++) {
                 u32x4 w = q_valid ? *(const u32x4 *)(src + c * 16 + hf * 8) : u32x4{0, 0, 0, 0};
@@ -207,12 +220,59 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
         }
     }
 
-    // ---- K / V^T tiles: global -> registers -> LDS, double buffered.
+    // ---- K / V^T tiles, double buffered in LDS.
     const uint16_t *kbase = p.k_plane + ((size_t)kh * p.kvT + k_row0) * HDK;
     const uint16_t *vbase = p.vt_plane + (size_t)kh * HD * p.kvT + k_row0;
-    u32x4 stK[C::KCH], stV[C::VCH];
+    const int last_chunk = ((k_len > 0 ? k_len - 1 : 0) / 8) * 8;   // start of the last valid 8-key chunk
+    u32x4 stK[DIRECT ? 1 : C::KCH], stV[DIRECT ? 1 : C::VCH];
 
-    auto gload = [&](int kb) {
+    // DIRECT: wave w fills LDS slots [(w*8 + j)*64, +64) of each 2048-slot tile with one
+    // global_load_lds per j. K slot s holds key s/32, chunk (s%32) ^ (key & 15); V^T slot s
+    // holds dim s/8, key chunk (s%8) ^ ((dim >> 1) & 7). Rows past the record are clamped to
+    // valid addresses (their scores are masked; their values are zeroed in LDS before use).
+    auto issue_direct = [&](int kb, int buf) {
+        uint16_t *Ks = smem + buf * C::STAGE;
+        uint16_t *Vs = Ks + C::KTILE;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int grp = wave * 8 + j;
+            const int key = grp * 2 + (lane >> 5);
+            const int c = (lane & 31) ^ (key & 15);
+            const int krow = min(kb + key, k_len - 1);
+            __builtin_amdgcn_global_load_lds((const void *)(kbase + (size_t)krow * HDK + c * 8),
+                                             (lds_void *)(Ks + grp * 512), 16, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int grp = wave * 8 + j;
+            const int d = grp * 8 + (lane >> 3);
+            const int c = (lane & 7) ^ ((d >> 1) & 7);
+            const int kk = min(kb + c * 8, last_chunk);
+            __builtin_amdgcn_global_load_lds((const void *)(vbase + (size_t)d * p.kvT + kk),
+                                             (lds_void *)(Vs + grp * 512), 16, 0, 0);
+        }
+    };
+    // Zero the V^T entries of keys >= k_len in a tail tile (DIRECT loads leave clamped copies).
+    auto zero_tail = [&](int kb, int buf) {
+        uint16_t *Vs = smem + buf * C::STAGE + C::KTILE;
+        const int valid = k_len - kb;   // 1..BK-1
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int s = tid + 256 * j;
+            const int d = s >> 3, c = (s & 7) ^ ((d >> 1) & 7);
+            const int k0 = c * 8;
+            if (k0 + 8 > valid) {
+                u32x4 w = *(u32x4 *)(Vs + s * 8);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if (k0 + 2 * e >= valid) w[e] = 0;
+                    else if (k0 + 2 * e + 1 >= valid) w[e] &= 0xffffu;
+                }
+                *(u32x4 *)(Vs + s * 8) = w;
+            }
+        }
+    };
+    auto gload = [&](int kb) {   // staged path: global -> registers
 #pragma unroll
         for (int j = 0; j < C::KCH; j++) {
             const int id = tid + 256 * j;
@@ -228,21 +288,12 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
             const int d = id / (BK / 8), c8 = id % (BK / 8);
             const int kk = kb + c8 * 8;
             u32x4 w = {0, 0, 0, 0};
-            if ((C::VCHUNKS % 256 == 0 || id < C::VCHUNKS) && kk < k_len) {
+            if ((C::VCHUNKS % 256 == 0 || id < C::VCHUNKS) && kk < k_len)
                 w = *(const u32x4 *)(vbase + (size_t)d * p.kvT + kk);
-                if (kk + 8 > k_len) {   // tail chunk: keys past the record are zero, never stale
-                    const int keep = k_len - kk;   // 1..7 valid bf16 values
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        if (2 * e >= keep) w[e] = 0;
-                        else if (2 * e + 1 >= keep) w[e] &= 0xffffu;
-                    }
-                }
-            }
             stV[j] = w;
         }
     };
-    auto sstore = [&](int buf) {
+    auto sstore = [&](int kb, int buf) {   // staged path: registers -> LDS, tail keys zeroed
         uint16_t *Ks = smem + buf * C::STAGE;
         uint16_t *Vs = Ks + C::KTILE;
 #pragma unroll
@@ -258,7 +309,17 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
             const int id = tid + 256 * j;
             if (C::VCHUNKS % 256 == 0 || id < C::VCHUNKS) {
                 const int d = id / (BK / 8), c8 = id % (BK / 8);
-                *(u32x4 *)(Vs + d * VROW + c8 * 8) = stV[j];
+                const int kk = kb + c8 * 8;
+                u32x4 w = stV[j];
+                if (kk + 8 > k_len) {   // keys past the record are zero, never stale
+                    const int keep = k_len - kk;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        if (2 * e >= keep) w[e] = 0;
+                        else if (2 * e + 1 >= keep) w[e] &= 0xffffu;
+                    }
+                }
+                *(u32x4 *)(Vs + d * VROW + c8 * 8) = w;
             }
         }
     };
@@ -272,16 +333,42 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
     const float sl2 = p.scale_log2;
     const int n_tiles = (k_len + BK - 1) / BK;
     const int prow = perm_row(lq);
+    // per-lane LDS element offsets of the A operands
+    //   DIRECT K: row (kt*32 + prow), chunk (2c + hf) ^ (prow & 15)  -> split c = 8*ch + cl
+    //   DIRECT V: row (mt*32 + prow), chunk (4kt + 2cc + hf) ^ ((prow >> 1) & 7)
+    int koff[8], voff[NKT][2];
+#pragma unroll
+    for (int cl = 0; cl < 8; cl++) {
+        koff[cl] = DIRECT ? prow * KROW + (((2 * cl + hf) ^ (prow & 15)) * 8) : prow * KROW + (2 * cl + hf) * 8;
+    }
+#pragma unroll
+    for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++)
+            voff[kt][cc] = DIRECT ? prow * VROW + (((4 * kt + 2 * cc + hf) ^ ((prow >> 1) & 7)) * 8)
+                                  : prow * VROW + kt * 32 + cc * 16 + hf * 8;
 
     if (n_tiles > 0) {
-        gload(0);
-        sstore(0);
+        if (DIRECT) {
+            issue_direct(0, 0);
+            __builtin_amdgcn_s_waitcnt(0);
+        } else {
+            gload(0);
+            sstore(0, 0);
+        }
     }
     __syncthreads();
     for (int t = 0; t < n_tiles; t++) {
         const int kb = t * BK;
         const int buf = t & 1;
-        if (t + 1 < n_tiles) gload(kb + BK);
+        if (DIRECT && kb + BK > k_len) {   // WG-uniform: only the block's last tile
+            zero_tail(kb, buf);
+            __syncthreads();
+        }
+        if (t + 1 < n_tiles) {
+            if (DIRECT) issue_direct(kb + BK, buf ^ 1);
+            else gload(kb + BK);
+        }
         const bool active = wave_live && (!p.causal || kb <= wave_last_pos);
         if (active) {
             const uint16_t *Ks = smem + buf * C::STAGE;
@@ -291,10 +378,10 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
             for (int kt = 0; kt < NKT; kt++) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) s[kt][i] = 0.f;
-                const uint16_t *kr = Ks + (kt * 32 + prow) * KROW + hf * 8;
 #pragma unroll
                 for (int c = 0; c < NC; c++) {
-                    const bf16x8 a = *(const bf16x8 *)(kr + c * 16);
+                    const int off = kt * 32 * KROW + (DIRECT ? (c >> 3) * 128 : (c >> 3) * 128) + koff[c & 7];
+                    const bf16x8 a = *(const bf16x8 *)(Ks + off);
                     s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c], s[kt], 0, 0, 0);
                 }
             }
@@ -347,17 +434,19 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
             }
 #pragma unroll
             for (int mt = 0; mt < NM; mt++) {
-                const uint16_t *vr = Vs + (mt * 32 + prow) * VROW + hf * 8;
 #pragma unroll
                 for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
                     for (int cc = 0; cc < 2; cc++) {
-                        const bf16x8 a = *(const bf16x8 *)(vr + kt * 32 + cc * 16);
+                        const bf16x8 a = *(const bf16x8 *)(Vs + mt * 32 * VROW + voff[kt][cc]);
                         o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[kt][cc], o[mt], 0, 0, 0);
                     }
             }
         }
-        if (t + 1 < n_tiles) sstore(buf ^ 1);
+        if (t + 1 < n_tiles) {
+            if (DIRECT) __builtin_amdgcn_s_waitcnt(0);
+            else sstore(kb + BK, buf ^ 1);
+        }
         __syncthreads();
     }
 
@@ -387,7 +476,6 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
             }
     }
 }
-
 // ------------------------------------------------------------------------------------------
 // Text K/V prologue (metal/clef.metal:245-300 and 873-928 for K and V): per kv row of the
 // plan, K = RMSNorm(k) * (1+w) then partial rotary, written to the K plane [nkv][kvT][HD];

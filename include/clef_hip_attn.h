@@ -84,7 +84,7 @@ bool clef_hip_vis_positions(const int32_t *cu, int n_img, const int32_t *grid_w,
 
 /* One full-attention layer of the dense text models (hd 256, GQA). */
 typedef struct {
-    int nh, nkv, hd, n_rot;   /* hd must be 256; n_rot in {0, 32, 64, 128, 256} */
+    int nh, nkv, hd, n_rot;   /* hd must be 256; n_rot 64 (Clef) or 0 */
     float eps, scale;         /* RMSNorm eps (1e-6), softmax scale (1/sqrt(hd)) */
     int T, row;               /* pass rows; qkv row stride in elements (multiple of 8) */
     const uint16_t *qkv;      /* [T][row] bf16 */
