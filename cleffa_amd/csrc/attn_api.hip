@@ -3,12 +3,14 @@
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
 #include <vector>
 
 #include "attn_kernels.h"
+#include "attn_text.h"
 #include "attn_params.h"
 #include "clef_hip_attn.h"
 
@@ -87,7 +89,7 @@ bool clef_hip_attn_init(char *err, size_t errlen) {
     if (e != hipSuccess) return fail(err, errlen, "device query failed: %s", hipGetErrorString(e));
     if (!strstr(prop.gcnArchName, "gfx950")) return fail(err, errlen, "kernels are built for gfx950, device is %s", prop.gcnArchName);
     if (prop.warpSize != 64) return fail(err, errlen, "attention kernels need 64-wide wavefronts (device reports %d)", prop.warpSize);
-    const size_t need = sizeof(uint16_t) * 2 * AttnCfg<256, 64, true>::STAGE;
+    const size_t need = sizeof(uint16_t) * text::LDS_ELEMS;
     if (prop.sharedMemPerBlock < need) return fail(err, errlen, "device LDS %zu < %zu bytes", (size_t)prop.sharedMemPerBlock, need);
     return true;
 }
@@ -208,9 +210,9 @@ bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, si
     const long grid = (long)a->n_blk * a->nh;
     if (grid > 0x7fffffffL) return fail(err, errlen, "grid too large");
     if (a->n_rot == 64)
-        hipLaunchKernelGGL((attn_fwd_kernel<256, 64, true, 64, true>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+        hipLaunchKernelGGL(attn_text_kernel<64>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);
     else
-        hipLaunchKernelGGL((attn_fwd_kernel<256, 64, true, 0, true>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+        hipLaunchKernelGGL(attn_text_kernel<0>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);
     return launch_ok("attn_fwd<256>", err, errlen);
 }
 
@@ -248,7 +250,7 @@ bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err,
     p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = a->f16_lim;
     p.causal = 0; p.gate = 0; p.out_type = a->out_type; p.out_ld = a->heads * kVisHD;
     (void)kVisHDK;
-    hipLaunchKernelGGL((attn_fwd_kernel<72, 64, false, 0, false>), dim3((unsigned)(a->n_blk * a->heads)), dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((attn_fwd_kernel<72, 64, false, 0, false, false>), dim3((unsigned)(a->n_blk * a->heads)), dim3(256), 0, (hipStream_t)stream, p);
     return launch_ok("attn_fwd<72>", err, errlen);
 }
 

@@ -54,6 +54,11 @@ __device__ __forceinline__ constexpr int out_off(int i, int hf) {
     return (i & 7) + 8 * hf + 16 * (i >> 3);
 }
 
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal (~1 ulp each).
+__device__ __forceinline__ float sigmoidf(float x) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
+
 __device__ __forceinline__ float wave_max_pair(float v) {
     return fmaxf(v, __shfl_xor(v, 32, 64));
 }
@@ -96,6 +101,8 @@ __device__ __forceinline__ void store_out8(void *out, size_t idx, const float *v
 //   TEXT   true: Q comes from the fused qkv rows with RMSNorm + rotary applied here and the
 //          sigmoid gate from the same rows; false: Q from a prepared plane, no gate.
 //   NROT   rotary dims of the text Q prologue (0 or a multiple of 32)
+//   PIPE   true: S(t+1) = K(t+1).Q^T is issued before the softmax of tile t so the MFMA and
+//          VALU work of neighbouring tiles can overlap (two score register sets).
 //   DIRECT true: K / V^T tiles go global -> LDS with global_load_lds (no VGPR staging) into
 //          unpadded, XOR-swizzled LDS rows; needs 512-byte K rows (HD 256). false: tiles are
 //          staged through VGPRs into padded LDS rows.
@@ -111,7 +118,7 @@ struct AttnCfg {
     static constexpr int VROW = DIRECT ? BK : BK + 8;     // LDS row stride of the V^T tile (elements)
     static constexpr int KTILE = BK * KROW;
     static constexpr int VTILE = HDM * VROW;
-    static constexpr int STAGE = KTILE + VTILE;
+    static constexpr int STAGE = KTILE + VTILE;   // one K + one V^T buffer
     static constexpr int KCHUNKS = BK * HDK / 8;  // 16-byte chunks per K tile
     static constexpr int VCHUNKS = HD * BK / 8;   // 16-byte chunks per V^T tile (HD rows)
     static constexpr int KCH = (KCHUNKS + 255) / 256;
@@ -121,7 +128,7 @@ struct AttnCfg {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int HD, int BK, bool TEXT, int NROT, bool DIRECT>
+template <int HD, int BK, bool TEXT, int NROT, bool DIRECT, bool PIPE>
 __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
     using C = AttnCfg<HD, BK, DIRECT>;
     constexpr int HDK = C::HDK, NC = C::NC, NM = C::NM, NKT = C::NKT;
@@ -220,82 +227,72 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
         }
     }
 
-    // ---- K / V^T tiles, double buffered in LDS.
+    // ---- K / V^T tiles in LDS: two K buffers, then two V^T buffers.
+    // Iteration t computes S(t+1) = K(t+1).Q^T on the MFMA pipe while the VALU runs the softmax
+    // of S(t), then O += V(t)^T.P(t); meanwhile K(t+2) and V(t+1) stream into the free buffers.
     const uint16_t *kbase = p.k_plane + ((size_t)kh * p.kvT + k_row0) * HDK;
     const uint16_t *vbase = p.vt_plane + (size_t)kh * HD * p.kvT + k_row0;
     const int last_chunk = ((k_len > 0 ? k_len - 1 : 0) / 8) * 8;   // start of the last valid 8-key chunk
     u32x4 stK[DIRECT ? 1 : C::KCH], stV[DIRECT ? 1 : C::VCH];
+    auto Kbuf = [&](int b) { return smem + b * C::KTILE; };
+    auto Vbuf = [&](int b) { return smem + 2 * C::KTILE + b * C::VTILE; };
 
     // DIRECT: wave w fills LDS slots [(w*8 + j)*64, +64) of each 2048-slot tile with one
     // global_load_lds per j. K slot s holds key s/32, chunk (s%32) ^ (key & 15); V^T slot s
     // holds dim s/8, key chunk (s%8) ^ ((dim >> 1) & 7). Rows past the record are clamped to
     // valid addresses (their scores are masked; their values are zeroed in LDS before use).
-    auto issue_direct = [&](int kb, int buf) {
-        uint16_t *Ks = smem + buf * C::STAGE;
-        uint16_t *Vs = Ks + C::KTILE;
+    // Staged (not DIRECT): global -> VGPRs now, VGPRs -> padded LDS rows in store_k / store_v.
+    auto load_k = [&](int kb, int b) {
+        if (DIRECT) {
+            uint16_t *Ks = Kbuf(b);
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int grp = wave * 8 + j;
-            const int key = grp * 2 + (lane >> 5);
-            const int c = (lane & 31) ^ (key & 15);
-            const int krow = min(kb + key, k_len - 1);
-            __builtin_amdgcn_global_load_lds((const void *)(kbase + (size_t)krow * HDK + c * 8),
-                                             (lds_void *)(Ks + grp * 512), 16, 0, 0);
-        }
+            for (int j = 0; j < 8; j++) {
+                const int grp = wave * 8 + j;
+                const int key = grp * 2 + (lane >> 5);
+                const int c = (lane & 31) ^ (key & 15);
+                const int krow = min(kb + key, k_len - 1);
+                __builtin_amdgcn_global_load_lds((const void *)(kbase + (size_t)krow * HDK + c * 8),
+                                                 (lds_void *)(Ks + grp * 512), 16, 0, 0);
+            }
+        } else {
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int grp = wave * 8 + j;
-            const int d = grp * 8 + (lane >> 3);
-            const int c = (lane & 7) ^ ((d >> 1) & 7);
-            const int kk = min(kb + c * 8, last_chunk);
-            __builtin_amdgcn_global_load_lds((const void *)(vbase + (size_t)d * p.kvT + kk),
-                                             (lds_void *)(Vs + grp * 512), 16, 0, 0);
-        }
-    };
-    // Zero the V^T entries of keys >= k_len in a tail tile (DIRECT loads leave clamped copies).
-    auto zero_tail = [&](int kb, int buf) {
-        uint16_t *Vs = smem + buf * C::STAGE + C::KTILE;
-        const int valid = k_len - kb;   // 1..BK-1
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int s = tid + 256 * j;
-            const int d = s >> 3, c = (s & 7) ^ ((d >> 1) & 7);
-            const int k0 = c * 8;
-            if (k0 + 8 > valid) {
-                u32x4 w = *(u32x4 *)(Vs + s * 8);
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    if (k0 + 2 * e >= valid) w[e] = 0;
-                    else if (k0 + 2 * e + 1 >= valid) w[e] &= 0xffffu;
-                }
-                *(u32x4 *)(Vs + s * 8) = w;
+            for (int j = 0; j < C::KCH; j++) {
+                const int id = tid + 256 * j;
+                const int key = id / (HDK / 8), c8 = id % (HDK / 8);
+                u32x4 w = {0, 0, 0, 0};
+                if ((C::KCHUNKS % 256 == 0 || id < C::KCHUNKS) && kb + key < k_len)
+                    w = *(const u32x4 *)(kbase + (size_t)(kb + key) * HDK + c8 * 8);
+                stK[j] = w;
             }
         }
     };
-    auto gload = [&](int kb) {   // staged path: global -> registers
+    auto load_v = [&](int kb, int b) {
+        if (DIRECT) {
+            uint16_t *Vs = Vbuf(b);
 #pragma unroll
-        for (int j = 0; j < C::KCH; j++) {
-            const int id = tid + 256 * j;
-            const int key = id / (HDK / 8), c8 = id % (HDK / 8);
-            u32x4 w = {0, 0, 0, 0};
-            if ((C::KCHUNKS % 256 == 0 || id < C::KCHUNKS) && kb + key < k_len)
-                w = *(const u32x4 *)(kbase + (size_t)(kb + key) * HDK + c8 * 8);
-            stK[j] = w;
-        }
+            for (int j = 0; j < 8; j++) {
+                const int grp = wave * 8 + j;
+                const int d = grp * 8 + (lane >> 3);
+                const int c = (lane & 7) ^ ((d >> 1) & 7);
+                const int kk = min(kb + c * 8, last_chunk);
+                __builtin_amdgcn_global_load_lds((const void *)(vbase + (size_t)d * p.kvT + kk),
+                                                 (lds_void *)(Vs + grp * 512), 16, 0, 0);
+            }
+        } else {
 #pragma unroll
-        for (int j = 0; j < C::VCH; j++) {
-            const int id = tid + 256 * j;
-            const int d = id / (BK / 8), c8 = id % (BK / 8);
-            const int kk = kb + c8 * 8;
-            u32x4 w = {0, 0, 0, 0};
-            if ((C::VCHUNKS % 256 == 0 || id < C::VCHUNKS) && kk < k_len)
-                w = *(const u32x4 *)(vbase + (size_t)d * p.kvT + kk);
-            stV[j] = w;
+            for (int j = 0; j < C::VCH; j++) {
+                const int id = tid + 256 * j;
+                const int d = id / (BK / 8), c8 = id % (BK / 8);
+                const int kk = kb + c8 * 8;
+                u32x4 w = {0, 0, 0, 0};
+                if ((C::VCHUNKS % 256 == 0 || id < C::VCHUNKS) && kk < k_len)
+                    w = *(const u32x4 *)(vbase + (size_t)d * p.kvT + kk);
+                stV[j] = w;
+            }
         }
     };
-    auto sstore = [&](int kb, int buf) {   // staged path: registers -> LDS, tail keys zeroed
-        uint16_t *Ks = smem + buf * C::STAGE;
-        uint16_t *Vs = Ks + C::KTILE;
+    auto store_k = [&](int b) {
+        uint16_t *Ks = Kbuf(b);
 #pragma unroll
         for (int j = 0; j < C::KCH; j++) {
             const int id = tid + 256 * j;
@@ -304,6 +301,9 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
                 *(u32x4 *)(Ks + key * KROW + c8 * 8) = stK[j];
             }
         }
+    };
+    auto store_v = [&](int kb, int b) {   // keys past the record are written as zeros
+        uint16_t *Vs = Vbuf(b);
 #pragma unroll
         for (int j = 0; j < C::VCH; j++) {
             const int id = tid + 256 * j;
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
                 const int d = id / (BK / 8), c8 = id % (BK / 8);
                 const int kk = kb + c8 * 8;
                 u32x4 w = stV[j];
-                if (kk + 8 > k_len) {   // keys past the record are zero, never stale
+                if (kk + 8 > k_len) {
                     const int keep = k_len - kk;
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
@@ -321,6 +321,24 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
                 }
                 *(u32x4 *)(Vs + d * VROW + c8 * 8) = w;
             }
+        }
+    };
+    // DIRECT tail tile: zero the V^T entries of keys >= k_len (the loads left clamped copies).
+    auto zero_tail = [&](int kb, int b) {
+        uint16_t *Vs = Vbuf(b);
+        const int valid = k_len - kb;   // 1..BK-1
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int s = tid + 256 * j;
+            const int d = s >> 3, c = (s & 7) ^ ((d >> 1) & 7);
+            const int k0 = c * 8;
+            u32x4 w = *(u32x4 *)(Vs + s * 8);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const unsigned keep = (k0 + 2 * e + 1 < valid) ? 0xffffffffu : (k0 + 2 * e < valid ? 0xffffu : 0u);
+                w[e] &= keep;
+            }
+            *(u32x4 *)(Vs + s * 8) = w;
         }
     };
 
@@ -334,13 +352,12 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
     const int n_tiles = (k_len + BK - 1) / BK;
     const int prow = perm_row(lq);
     // per-lane LDS element offsets of the A operands
-    //   DIRECT K: row (kt*32 + prow), chunk (2c + hf) ^ (prow & 15)  -> split c = 8*ch + cl
-    //   DIRECT V: row (mt*32 + prow), chunk (4kt + 2cc + hf) ^ ((prow >> 1) & 7)
-    int koff[8], voff[NKT][2];
+    //   K: row (kt*32 + prow), 16-byte chunk 2c + hf, c = 8*ch + cl (DIRECT: chunk ^ (prow & 15))
+    //   V: row (mt*32 + prow), chunk 4kt + 2cc + hf (DIRECT: chunk ^ ((prow >> 1) & 7))
+    int koff[C::NC < 8 ? C::NC : 8], voff[NKT][2];
 #pragma unroll
-    for (int cl = 0; cl < 8; cl++) {
+    for (int cl = 0; cl < (NC < 8 ? NC : 8); cl++)
         koff[cl] = DIRECT ? prow * KROW + (((2 * cl + hf) ^ (prow & 15)) * 8) : prow * KROW + (2 * cl + hf) * 8;
-    }
 #pragma unroll
     for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
@@ -348,60 +365,57 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
             voff[kt][cc] = DIRECT ? prow * VROW + (((4 * kt + 2 * cc + hf) ^ ((prow >> 1) & 7)) * 8)
                                   : prow * VROW + kt * 32 + cc * 16 + hf * 8;
 
-    if (n_tiles > 0) {
-        if (DIRECT) {
-            issue_direct(0, 0);
-            __builtin_amdgcn_s_waitcnt(0);
-        } else {
-            gload(0);
-            sstore(0, 0);
+    auto act = [&](int t) { return wave_live && (!p.causal || t * BK <= wave_last_pos); };
+    auto qk = [&](int b, f32x16 *s) {
+        const uint16_t *Ks = Kbuf(b);
+#pragma unroll
+        for (int kt = 0; kt < NKT; kt++) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) s[kt][i] = 0.f;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const bf16x8 a = *(const bf16x8 *)(Ks + kt * 32 * KROW + (c >> 3) * 128 + koff[c & 7]);
+                s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c], s[kt], 0, 0, 0);
+            }
         }
-    }
-    __syncthreads();
-    for (int t = 0; t < n_tiles; t++) {
+    };
+
+    auto tile = [&](int t, f32x16 *s_cur, f32x16 *s_nxt) {
         const int kb = t * BK;
-        const int buf = t & 1;
+        const int vb = t & 1;
         if (DIRECT && kb + BK > k_len) {   // WG-uniform: only the block's last tile
-            zero_tail(kb, buf);
+            zero_tail(kb, vb);
             __syncthreads();
         }
-        if (t + 1 < n_tiles) {
-            if (DIRECT) issue_direct(kb + BK, buf ^ 1);
-            else gload(kb + BK);
+        if (PIPE) {
+            if (t + 2 < n_tiles) load_k(kb + 2 * BK, vb);
+            if (t + 1 < n_tiles) load_v(kb + BK, vb ^ 1);
+            if (t + 1 < n_tiles && act(t + 1)) qk(vb ^ 1, s_nxt);
+        } else if (t + 1 < n_tiles) {
+            load_k(kb + BK, vb ^ 1);
+            load_v(kb + BK, vb ^ 1);
         }
-        const bool active = wave_live && (!p.causal || kb <= wave_last_pos);
-        if (active) {
-            const uint16_t *Ks = smem + buf * C::STAGE;
-            const uint16_t *Vs = Ks + C::KTILE;
-            f32x16 s[NKT];
-#pragma unroll
-            for (int kt = 0; kt < NKT; kt++) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) s[kt][i] = 0.f;
-#pragma unroll
-                for (int c = 0; c < NC; c++) {
-                    const int off = kt * 32 * KROW + (DIRECT ? (c >> 3) * 128 : (c >> 3) * 128) + koff[c & 7];
-                    const bf16x8 a = *(const bf16x8 *)(Ks + off);
-                    s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c], s[kt], 0, 0, 0);
-                }
-            }
+        if (act(t)) {
+            if (!PIPE) qk(vb, s_cur);
+            const uint16_t *Vs = Vbuf(vb);
             // Online softmax in the exp2 domain. Masked scores are -inf, so their P is an
-            // exact zero and a tile past a row's diagonal rescales it by exactly 1.
+            // exact zero and a tile past a row's diagonal rescales the row by exactly 1.
             const bool need_mask = (kb + BK > k_len) || (p.causal && kb + BK - 1 > q_pos0 + wave * 32);
+            if (need_mask) {
+                // key kb + kt*32 + out_off(i, hf) is visible iff <= lim
+                const int lim = min(k_len - 1, p.causal ? qpos : k_len - 1) - kb - 8 * hf;
+#pragma unroll
+                for (int kt = 0; kt < NKT; kt++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++)
+                        s_cur[kt][i] = (kt * 32 + (i & 7) + 16 * (i >> 3) > lim) ? -INFINITY : s_cur[kt][i];
+            }
             float mx = -INFINITY;
 #pragma unroll
             for (int kt = 0; kt < NKT; kt++)
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    float v = s[kt][i] * sl2;
-                    if (need_mask) {
-                        const int key = kb + kt * 32 + out_off(i, hf);
-                        if (key >= k_len || (p.causal && key > qpos)) v = -INFINITY;
-                    }
-                    s[kt][i] = v;
-                    mx = fmaxf(mx, v);
-                }
-            mx = wave_max_pair(mx);
+                for (int i = 0; i < 16; i++) mx = fmaxf(mx, s_cur[kt][i]);
+            mx = wave_max_pair(mx) * sl2;
             const float mn = fmaxf(m_run, mx);
             const float msub = (mn == -INFINITY) ? 0.f : mn;
             const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
@@ -414,11 +428,12 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
                     unsigned w[4];
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
-                        const float p0 = __builtin_amdgcn_exp2f(s[kt][cc * 8 + 2 * j] - msub);
-                        const float p1 = __builtin_amdgcn_exp2f(s[kt][cc * 8 + 2 * j + 1] - msub);
+                        const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[kt][cc * 8 + 2 * j], sl2, -msub));
+                        const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[kt][cc * 8 + 2 * j + 1], sl2, -msub));
                         w[j] = pack_bf16(p0, p1);
                         // The row sum takes the rounded P that the PV product multiplies.
-                        rs += bf_lo(w[j]) + bf_hi(w[j]);
+                        rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]),
+                                                             bf16x2{(__bf16)1.0f, (__bf16)1.0f}, rs, false);
                     }
                     u32x4 wv = {w[0], w[1], w[2], w[3]};
                     pk[kt][cc] = __builtin_bit_cast(bf16x8, wv);
@@ -443,11 +458,37 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
                     }
             }
         }
-        if (t + 1 < n_tiles) {
-            if (DIRECT) __builtin_amdgcn_s_waitcnt(0);
-            else sstore(kb + BK, buf ^ 1);
+        if (!DIRECT) {
+            if (PIPE ? t + 2 < n_tiles : t + 1 < n_tiles) store_k(PIPE ? vb : vb ^ 1);
+            if (t + 1 < n_tiles) store_v(kb + BK, vb ^ 1);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);
         }
         __syncthreads();
+    };
+
+    f32x16 s0[NKT], s1[NKT];
+    if (n_tiles > 0) {
+        load_k(0, 0);
+        if (!DIRECT) store_k(0);
+        load_v(0, 0);
+        if (!DIRECT) store_v(0, 0);
+        if (PIPE && n_tiles > 1) {
+            load_k(BK, 1);
+            if (!DIRECT) store_k(1);
+        }
+        if (DIRECT) __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (PIPE && act(0)) qk(0, s0);
+    }
+    if (PIPE) {
+        // two tiles per trip so the score registers swap roles without copies
+        for (int t = 0; t < n_tiles; t += 2) {
+            tile(t, s0, s1);
+            if (t + 1 < n_tiles) tile(t + 1, s1, s0);
+        }
+    } else {
+        for (int t = 0; t < n_tiles; t++) tile(t, s0, s0);
     }
 
     // ---- Epilogue: O / l, times sigmoid(gate) for text, converted and stored.
@@ -468,8 +509,8 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
                     const u32x4 g = *(const u32x4 *)(p.qkv + t * p.row + (size_t)h * 2 * HD + HD + d0);
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
-                        v[2 * j] *= 1.f / (1.f + expf(-bf_lo(g[j])));
-                        v[2 * j + 1] *= 1.f / (1.f + expf(-bf_hi(g[j])));
+                        v[2 * j] *= sigmoidf(bf_lo(g[j]));
+                        v[2 * j + 1] *= sigmoidf(bf_hi(g[j]));
                     }
                 }
                 store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);

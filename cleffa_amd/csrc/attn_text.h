@@ -1,0 +1,320 @@
+// Text prefill attention for head dim 256 on CDNA4: packed varlen causal GQA attention over a
+// record-aligned block list, with the Q prologue (per-head RMSNorm + partial interleaved
+// M-RoPE) fused into the block's start and the sigmoid output gate fused into the epilogue.
+// Semantics: metal/clef.metal:930-1093 (attention_tu: block list, record-aligned key tiles,
+// sum of the rounded P, O / l * sigmoid(G)), metal/clef.metal:245-300 (prologue),
+// metal/clef.metal:709-849 (prefix: queries offset into the record's keys).
+//
+// Workgroup: 8 wavefronts (2 per SIMD), one block of 128 query rows of one q head; wave w owns
+// rows 16w .. 16w+15. Everything per wave lives in ~170 VGPRs (O^T 64, Q 32, S 16), so two
+// waves share a SIMD and one wave's softmax overlaps the other's matrix work.
+//   S^T = K . Q^T      v_mfma_f32_16x16x32_bf16: A = 16 keys x 32 dims of K from LDS,
+//                      B = the wave's Q (registers). A lane owns one query column.
+//   O^T += V^T . P^T   A = 16 dims x 32 keys of V^T from LDS, B = P straight from registers.
+// The A rows are read in a permuted order (key / dim 8*(r/4) + 4*(tile&1) + r%4 for row r) so
+// that the 8 keys a lane's P covers and the 8 dims its O covers are consecutive: P is the next
+// product's B operand with no shuffle, and the epilogue stores 16-byte runs.
+// K and V^T tiles (64 keys) stream global -> LDS with global_load_lds, double buffered, into
+// unpadded rows whose 16-byte chunks are XOR-swizzled so the A reads are bank-conflict free.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attn_kernels.h"
+#include "attn_params.h"
+
+namespace clef_hip {
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+namespace text {
+constexpr int HD = 256;                 // head dim
+constexpr int BQ = 128;                 // query rows per block
+constexpr int BK = 64;                  // keys per LDS tile
+constexpr int WAVES = 8;
+constexpr int ROWS = 16;                // query rows per wave
+constexpr int NC = HD / 32;             // 32-dim contraction chunks of S
+constexpr int KTILE = BK * HD;          // elements per K tile  (32 KB)
+constexpr int VTILE = HD * BK;          // elements per V^T tile (32 KB)
+constexpr int LDS_ELEMS = 2 * KTILE + 2 * VTILE;   // 128 KB
+
+// key of A-operand row r in S tile kt (four 16-key tiles per 64-key LDS tile)
+__device__ __forceinline__ int s_row_key(int kt, int r) {
+    return 32 * (kt >> 1) + 8 * (r >> 2) + 4 * (kt & 1) + (r & 3);
+}
+// XOR swizzle of a K row's 16-byte chunks (rows of 32 chunks); distinct over the 16 keys
+// that one A read touches
+__device__ __forceinline__ int k_swz(int key) { return (key & 15) ^ ((key >> 4) << 2); }
+// XOR swizzle of a V^T row's chunks (rows of 8 chunks, two rows per 256-byte bank line)
+__device__ __forceinline__ int v_swz(int d) { return ((d >> 1) & 1) | (((d >> 3) & 3) << 1); }
+}  // namespace text
+
+template <int NROT>
+__global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
+    using namespace text;
+    static_assert(NROT % 64 == 0 && NROT <= HD, "rotary pairs must sit in one lane");
+    __shared__ __attribute__((aligned(16))) uint16_t smem[LDS_ELEMS];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int q16 = lane & 15, g = lane >> 4;
+
+    const int bi = blockIdx.x / p.nh;
+    const int h = blockIdx.x - bi * p.nh;
+    const int32_t *blk = p.blocks + 8 * bi;
+    const int q_row0 = blk[0], nq = blk[1], q_pos0 = blk[2], k_row0 = blk[3], k_len = blk[4];
+    const int flag_row = blk[5];
+    const int kh = h / (p.nh / p.nkv);
+
+    const int my_q = wave * ROWS + q16;
+    const bool q_valid = my_q < nq;
+    const int qpos = q_pos0 + my_q;
+    const bool wave_live = wave * ROWS < nq;
+    const int wave_last_pos = q_pos0 + wave * ROWS + ROWS - 1;
+    const size_t qrow = (size_t)q_row0 + (q_valid ? my_q : 0);
+
+    // ---- Q prologue: lane holds Q[my_q][c*32 + 8g + j], the B operand of chunk c.
+    bf16x8 qf[NC];
+    {
+        float x[NC][8];
+        const uint16_t *src = p.qkv + qrow * p.row + (size_t)h * 2 * HD;
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            u32x4 w = q_valid ? *(const u32x4 *)(src + c * 32 + 8 * g) : u32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                x[c][2 * j] = bf_lo(w[j]);
+                x[c][2 * j + 1] = bf_hi(w[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) ss += x[c][j] * x[c][j];
+        }
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        if (p.q_norm) {   // NULL: no q/k norm (plain SDPA operands)
+            const float inv = rsqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const float4 w0 = *(const float4 *)(p.q_norm + c * 32 + 8 * g);
+                const float4 w1 = *(const float4 *)(p.q_norm + c * 32 + 8 * g + 4);
+                const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) x[c][j] = x[c][j] * inv * wn[j];
+            }
+        }
+        if (NROT > 0) {
+            // NeoX partial rotary: pair (i, i + NROT/2) sits in this lane at chunks c and c + R.
+            // Interleaved M-RoPE: pair i turns by axis i % 3 of pos3.
+            constexpr int R = NROT / 64;
+            const int32_t *pp = p.pos3 + 3 * qrow;
+            const float pt = (float)pp[0], ph = (float)pp[1], pw = (float)pp[2];
+#pragma unroll
+            for (int c = 0; c < R; c++) {
+                const float4 f0 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g);
+                const float4 f1 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g + 4);
+                const float fr[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int i = c * 32 + 8 * g + j;
+                    const int ax = i % 3;
+                    const float pos = ax == 0 ? pt : (ax == 1 ? ph : pw);
+                    float sn, cs;
+                    sincosf(pos * fr[j], &sn, &cs);
+                    const float x0 = x[c][j], x1 = x[c + R][j];
+                    x[c][j] = x0 * cs - x1 * sn;
+                    x[c + R][j] = x1 * cs + x0 * sn;
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            u32x4 w = {pack_bf16(x[c][0], x[c][1]), pack_bf16(x[c][2], x[c][3]),
+                       pack_bf16(x[c][4], x[c][5]), pack_bf16(x[c][6], x[c][7])};
+            qf[c] = __builtin_bit_cast(bf16x8, w);
+        }
+    }
+
+    // ---- tiles
+    const uint16_t *kbase = p.k_plane + ((size_t)kh * p.kvT + k_row0) * HD;
+    const uint16_t *vbase = p.vt_plane + (size_t)kh * HD * p.kvT + k_row0;
+    const int last_chunk = ((k_len > 0 ? k_len - 1 : 0) / 8) * 8;
+    auto Kbuf = [&](int b) { return smem + b * KTILE; };
+    auto Vbuf = [&](int b) { return smem + 2 * KTILE + b * VTILE; };
+
+    // Wave w fills slots [(4w + j) * 64, +64) of each 2048-slot tile, one global_load_lds per j.
+    // K slot s: key s/32, chunk (s%32) ^ k_swz(key). V^T slot s: dim s/8, chunk (s%8) ^ v_swz(dim).
+    // Rows past the record are clamped to valid addresses; their scores are masked and their
+    // values zeroed in LDS before use.
+    auto load_tiles = [&](int kb, int b) {
+        uint16_t *Ks = Kbuf(b), *Vs = Vbuf(b);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int grp = wave * 4 + j;
+            const int key = grp * 2 + (lane >> 5);
+            const int c = (lane & 31) ^ k_swz(key);
+            const int krow = min(kb + key, k_len - 1);
+            __builtin_amdgcn_global_load_lds((const void *)(kbase + (size_t)krow * HD + c * 8),
+                                             (lds_void *)(Ks + grp * 512), 16, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int grp = wave * 4 + j;
+            const int d = grp * 8 + (lane >> 3);
+            const int c = (lane & 7) ^ v_swz(d);
+            const int kk = min(kb + c * 8, last_chunk);
+            __builtin_amdgcn_global_load_lds((const void *)(vbase + (size_t)d * p.kvT + kk),
+                                             (lds_void *)(Vs + grp * 512), 16, 0, 0);
+        }
+    };
+    auto zero_tail = [&](int kb, int b) {   // V^T entries of keys >= k_len -> 0
+        uint16_t *Vs = Vbuf(b);
+        const int valid = k_len - kb;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int s = tid + 512 * j;
+            const int d = s >> 3, c = (s & 7) ^ v_swz(d);
+            const int k0 = c * 8;
+            u32x4 w = *(u32x4 *)(Vs + s * 8);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const unsigned keep = (k0 + 2 * e + 1 < valid) ? 0xffffffffu : (k0 + 2 * e < valid ? 0xffffu : 0u);
+                w[e] &= keep;
+            }
+            *(u32x4 *)(Vs + s * 8) = w;
+        }
+    };
+
+    // per-lane LDS element offsets of the A operands
+    int koff[4][4];   // [S tile kt][c & 3]; chunk 4c + g of key s_row_key(kt, q16)
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+        const int key = s_row_key(kt, q16);
+        const int x = k_swz(key);
+#pragma unroll
+        for (int cl = 0; cl < 4; cl++) koff[kt][cl] = key * HD + (((4 * cl + g) ^ x) * 8);
+    }
+    const int vrow = 8 * (q16 >> 2) + (q16 & 3);   // + 32*(mt>>1) + 4*(mt&1)
+    const int vx = v_swz(vrow);                      // the mt part does not change the swizzle
+    const int voff0 = vrow * BK + ((g ^ vx) * 8);
+    const int voff1 = vrow * BK + (((4 + g) ^ vx) * 8);
+
+    f32x4 o[16];
+#pragma unroll
+    for (int mt = 0; mt < 16; mt++) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+    const float sl2 = p.scale_log2;
+    const int n_tiles = (k_len + BK - 1) / BK;
+
+    if (n_tiles > 0) {
+        load_tiles(0, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < n_tiles; t++) {
+        const int kb = t * BK;
+        const int b = t & 1;
+        if (kb + BK > k_len) {   // WG-uniform: the block's last tile
+            zero_tail(kb, b);
+            __syncthreads();
+        }
+        if (t + 1 < n_tiles) load_tiles(kb + BK, b ^ 1);
+        if (wave_live && (!p.causal || kb <= wave_last_pos)) {
+            const uint16_t *Ks = Kbuf(b), *Vs = Vbuf(b);
+            f32x4 s[4];
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+                s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const bf16x8 a = *(const bf16x8 *)(Ks + koff[kt][c & 3] + (c >> 2) * 128);
+                    s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[kt], 0, 0, 0);
+                }
+            }
+            // Online softmax in the exp2 domain. Masked scores are -inf, so their P is an exact
+            // zero and a tile past a row's diagonal rescales the row by exactly 1.
+            if ((kb + BK > k_len) || (p.causal && kb + BK - 1 > q_pos0 + wave * ROWS)) {
+                // element (kt, i) is key kb + 32(kt>>1) + 8g + 4(kt&1) + i
+                const int lim = min(k_len - 1, p.causal ? qpos : k_len - 1) - kb - 8 * g;
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        s[kt][i] = (32 * (kt >> 1) + 4 * (kt & 1) + i > lim) ? -INFINITY : s[kt][i];
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kt][i]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+            const float mn = fmaxf(m_run, mx);
+            const float msub = (mn == -INFINITY) ? 0.f : mn;
+            const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
+            float rs = 0.f;
+            bf16x8 pk[2];
+#pragma unroll
+            for (int kc = 0; kc < 2; kc++) {
+                unsigned w[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int kt = 2 * kc + (j >> 1), i = 2 * (j & 1);
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][i], sl2, -msub));
+                    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][i + 1], sl2, -msub));
+                    w[j] = pack_bf16(p0, p1);
+                    // the row sum takes the rounded P that the PV product multiplies
+                    rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]),
+                                                         bf16x2{(__bf16)1.0f, (__bf16)1.0f}, rs, false);
+                }
+                u32x4 wv = {w[0], w[1], w[2], w[3]};
+                pk[kc] = __builtin_bit_cast(bf16x8, wv);
+            }
+            rs += __shfl_xor(rs, 16, 64);
+            rs += __shfl_xor(rs, 32, 64);
+            l_run = l_run * alpha + rs;
+            m_run = mn;
+            if (__any(alpha != 1.f)) {
+#pragma unroll
+                for (int mt = 0; mt < 16; mt++) o[mt] *= alpha;
+            }
+#pragma unroll
+            for (int mt = 0; mt < 16; mt++) {
+                const int base = (32 * (mt >> 1) + 4 * (mt & 1)) * BK;
+                const bf16x8 a0 = *(const bf16x8 *)(Vs + base + voff0);
+                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, pk[0], o[mt], 0, 0, 0);
+                const bf16x8 a1 = *(const bf16x8 *)(Vs + base + voff1);
+                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, pk[1], o[mt], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+
+    // ---- Epilogue: O / l times sigmoid(gate); lane (q16, g) holds dims 32u + 8g + [0, 8).
+    if (q_valid) {
+        const float il = l_run > 0.f ? 1.f / l_run : 0.f;
+        const size_t t = (size_t)q_row0 + my_q;
+        int32_t *flag = p.ovf ? p.ovf + flag_row : nullptr;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int d0 = 32 * u + 8 * g;
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[i] = o[2 * u][i] * il;
+                v[4 + i] = o[2 * u + 1][i] * il;
+            }
+            if (p.gate) {
+                const u32x4 gw = *(const u32x4 *)(p.qkv + t * p.row + (size_t)h * 2 * HD + HD + d0);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    v[2 * j] *= sigmoidf(bf_lo(gw[j]));
+                    v[2 * j + 1] *= sigmoidf(bf_hi(gw[j]));
+                }
+            }
+            store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);
+        }
+    }
+}
+
+}  // namespace clef_hip
