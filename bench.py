@@ -65,7 +65,8 @@ def build_step(cfg, seed):
         kvT = plan.kvT
         kp, vt = att.planes(kvT)
     out = torch.empty((plan.T, w["nh"] * w["hd"]), dtype=torch.bfloat16, device=dev)
-    kwargs = dict(out=out, gate=w["gate"], k_plane=kp, vt_plane=vt, kvT=kvT)
+    kwargs = dict(out=out, gate=w["gate"], k_plane=kp, vt_plane=vt, kvT=kvT,
+                  rope_cs=att.rope_table(plan.T) if w["n_rot"] else None)
     args = (w["qkv"], w["q_norm"], w["k_norm"], w["pos3"], plan)
     step = lambda: att.forward(*args, stage="prefill", **kwargs)
     core = lambda: att.forward(*args, stage="core", **kwargs)

@@ -129,6 +129,24 @@ class AttnPlan:
         # kv rows the planes must hold, rounded to the 16-byte V^T chunk
         self.kvT = max(8, (self.kv_rows + 7) // 8 * 8)
 
+    def schedule(self, nh, n_slots):
+        """Persistent-workgroup schedule of this plan's (block, head) items over n_slots slots
+        (host-built, cached per (nh, n_slots)); returns (items, slot_off) device tensors."""
+        key = (nh, n_slots)
+        if not hasattr(self, "_sched"):
+            self._sched = {}
+        if key not in self._sched:
+            lib = _lib.load()
+            items = np.zeros(max(self.n_blk * nh, 1), dtype=np.int32)
+            off = np.zeros(n_slots + 1, dtype=np.int32)
+            err = _err()
+            blocks = np.ascontiguousarray(self.blocks_host if self.n_blk else np.zeros((1, BLOCK_INTS), np.int32))
+            _lib.check(lib.clef_hip_attn_schedule(_i32p(blocks), self.n_blk, nh, n_slots, _i32p(items),
+                                                  _i32p(off), err, len(err)), err)
+            self._sched[key] = (items[: self.n_blk * nh].copy(), off.copy(),
+                                torch.from_numpy(items).to(self.device), torch.from_numpy(off).to(self.device))
+        return self._sched[key]
+
     def pairs(self):
         """(query, key) pairs the plan visits under its mask: the algorithmic work unit."""
         total = 0
@@ -158,12 +176,16 @@ def _check(t, name, shape, dtype, device):
 class TextAttention:
     """One gated full-attention layer of the dense Clef models (hd 256, GQA)."""
 
-    def __init__(self, nh, nkv, hd=256, n_rot=64, eps=1e-6, rope_theta=1e7, device="cuda"):
+    def __init__(self, nh, nkv, hd=256, n_rot=64, eps=1e-6, rope_theta=1e7, device="cuda",
+                 persistent=False):
+        """persistent: run the attention kernel as one workgroup per compute unit over a
+        host-balanced schedule (False: one workgroup per (block, head) item)."""
         self.nh, self.nkv, self.hd, self.n_rot, self.eps = nh, nkv, hd, n_rot, eps
         self.scale = 1.0 / math.sqrt(hd)
         self.row = 2 * nh * hd + 2 * nkv * hd
         self.device = _device(device)
         init_device(self.device)
+        self.slots = torch.cuda.get_device_properties(self.device).multi_processor_count if persistent else 0
         self.inv_freq = torch.from_numpy(rope_inv_freq(rope_theta, n_rot).copy()).to(self.device) \
             if n_rot else torch.zeros(1, dtype=torch.float32, device=self.device)
 
@@ -173,8 +195,12 @@ class TextAttention:
         vt = torch.empty((self.nkv, self.hd, kvT), dtype=torch.bfloat16, device=self.device)
         return k, vt
 
+    def rope_table(self, T):
+        """[T][n_rot/2][2] f32 scratch for the rotary cos/sin of each pass row."""
+        return torch.empty((max(T, 1), max(self.n_rot // 2, 1), 2), dtype=torch.float32, device=self.device)
+
     def args(self, qkv, q_norm, k_norm, pos3, plan, out, k_plane, vt_plane, kvT,
-             out_type=OUT_BF16, gate=True, ovf=None, f16_lim=65504.0):
+             out_type=OUT_BF16, gate=True, ovf=None, f16_lim=65504.0, rope_cs=None, trace=None):
         T = plan.T
         dev = self.device
         _check(qkv, "qkv", (T, qkv.shape[1] if qkv.dim() == 2 else -1), torch.bfloat16, dev)
@@ -195,6 +221,8 @@ class TextAttention:
                                                     OUT_F32: torch.float32}[out_type], dev)
         if ovf is not None:
             _check(ovf, "ovf", (T,), torch.int32, dev)
+        if rope_cs is not None:
+            _check(rope_cs, "rope_cs", (max(T, 1), max(self.n_rot // 2, 1), 2), torch.float32, dev)
         if plan.device != dev:
             raise ValueError("plan lives on another device")
         if plan.n_blk:
@@ -206,18 +234,24 @@ class TextAttention:
         a.eps, a.scale = self.eps, self.scale
         a.T, a.row = T, qkv.shape[1]
         a.qkv, a.q_norm, a.k_norm = _ptr(qkv), _ptr(q_norm), _ptr(k_norm)
-        a.pos3, a.inv_freq = _ptr(pos3), _ptr(self.inv_freq)
+        a.pos3, a.inv_freq, a.rope_cs = _ptr(pos3), _ptr(self.inv_freq), _ptr(rope_cs)
         a.k_plane, a.vt_plane, a.kvT = _ptr(k_plane), _ptr(vt_plane), kvT
         a.blocks, a.n_blk = _ptr(plan.blocks), plan.n_blk
+        if self.slots > 0 and plan.n_blk:
+            _, _, items, off = plan.schedule(self.nh, self.slots)
+            a.sched, a.sched_off, a.n_slots = _ptr(items), _ptr(off), self.slots
         a.kv_tok, a.kv_rows = _ptr(plan.kv_tok), plan.kv_rows
         a.causal, a.gate = int(plan.causal), int(gate)
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
+        a.trace = _ptr(trace)
         return a
 
     def forward(self, qkv, q_norm, k_norm, pos3, plan, out=None, out_dtype="bf16", gate=True,
                 k_plane=None, vt_plane=None, kvT=None, ovf=None, f16_lim=65504.0, stream=None,
-                stage="prefill"):
-        """Runs one layer's attention. stage: "prefill" (prep_kv + core), "prep", or "core"."""
+                stage="prefill", rope_cs=None, trace=None):
+        """Runs one layer's attention. stage: "prefill" (prep_kv + core), "prep", or "core".
+        rope_cs: the rotary cos/sin scratch (see rope_table); allocated here for "prefill" when
+        not given. A "core" call with a table reads what the last "prep" call wrote."""
         lib = _lib.load()
         out_type, odt = _OUT_TYPES[out_dtype]
         if out is None:
@@ -227,8 +261,11 @@ class TextAttention:
             k_plane, vt_plane = self.planes(kvT)
         elif kvT is None:
             kvT = k_plane.shape[1]
+        if rope_cs is None and stage == "prefill" and self.n_rot:
+            rope_cs = self.rope_table(plan.T)
         a = self.args(qkv, q_norm, k_norm, pos3, plan, out, k_plane, vt_plane, kvT,
-                      out_type=out_type, gate=gate, ovf=ovf, f16_lim=f16_lim)
+                      out_type=out_type, gate=gate, ovf=ovf, f16_lim=f16_lim, rope_cs=rope_cs,
+                      trace=trace)
         fn = {"prefill": lib.clef_hip_attn_prefill, "prep": lib.clef_hip_attn_prep_kv,
               "core": lib.clef_hip_attn_core}[stage]
         err = _err()

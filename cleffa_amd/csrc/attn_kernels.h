@@ -521,74 +521,117 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
 // Text K/V prologue (metal/clef.metal:245-300 and 873-928 for K and V): per kv row of the
 // plan, K = RMSNorm(k) * (1+w) then partial rotary, written to the K plane [nkv][kvT][HD];
 // V copied unnormalised and written transposed to the V^T plane [nkv][HD][kvT]. Rows whose
-// kv_tok is negative (cached prefix rows, alignment padding) are left untouched.
-// Grid (kv_rows / 64, nkv), 256 threads; each wave handles 16 rows, a lane 4 dims.
+// kv_tok is negative (cached prefix rows, alignment padding) are left untouched. When rope_cs
+// is set, the cos/sin of every pass row's rotary angles are also written there ([T][n_rot/2]
+// float2) for the attention kernel's Q prologue.
+// Grid (kv_rows / 16, nkv), 256 threads. A row is handled by 32 lanes with 8 dims each
+// (16-byte loads and stores); the RMS sum reduces over DPP rows, a rotary pair (i, i + 32)
+// sits in lanes 4 apart.
 // ------------------------------------------------------------------------------------------
+__device__ __forceinline__ float row16_sum(float v) {   // sum over the lane's 16-lane row
+    v += __builtin_amdgcn_update_dpp(0.f, v, 0x128, 0xf, 0xf, false);   // row_ror:8
+    v += __builtin_amdgcn_update_dpp(0.f, v, 0x124, 0xf, 0xf, false);   // row_ror:4
+    v += __builtin_amdgcn_update_dpp(0.f, v, 0x4e, 0xf, 0xf, false);    // quad_perm [2,3,0,1]
+    v += __builtin_amdgcn_update_dpp(0.f, v, 0xb1, 0xf, 0xf, false);    // quad_perm [1,0,3,2]
+    return v;
+}
+
 __global__ __launch_bounds__(256) void text_prep_kv_kernel(PrepParams p) {
-    constexpr int HD = 256, ROWS = 64;
-    __shared__ __attribute__((aligned(16))) uint16_t vt[HD * (ROWS + 8)];
+    constexpr int HD = 256, ROWS = 16;           // kv rows per workgroup
+    constexpr int VS = HD + 8;                   // LDS row stride of the V tile
+    __shared__ __attribute__((aligned(16))) uint16_t vr[ROWS * VS];
     __shared__ int toks[ROWS];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x;
+    const int c = tid & 31, rl = tid >> 5;       // 8-dim chunk of the row, row within a pass
     const int row0 = blockIdx.x * ROWS, kh = blockIdx.y;
     if (tid < ROWS) toks[tid] = (row0 + tid < p.kv_rows) ? p.kv_tok[row0 + tid] : -1;
     __syncthreads();
-    const int half_rot = p.n_rot / 2;
-    for (int r = wave * 16; r < wave * 16 + 16; r++) {
-        const int tok = toks[r];
-        if (tok < 0) continue;
-        const uint16_t *src = p.qkv + (size_t)tok * p.row + (size_t)p.nh * 2 * HD + (size_t)kh * HD;
-        const u32x2 w = *(const u32x2 *)(src + 4 * lane);
-        float x[4] = {bf_lo(w[0]), bf_hi(w[0]), bf_lo(w[1]), bf_hi(w[1])};
-        float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+    u32x4 kw[2], vw[2];
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off, 64);
-        if (p.k_norm) {
-            const float inv = rsqrtf(ss / (float)HD + p.eps);
-            const float4 wn = *(const float4 *)(p.k_norm + 4 * lane);
-            x[0] *= inv * wn.x; x[1] *= inv * wn.y; x[2] *= inv * wn.z; x[3] *= inv * wn.w;
+    for (int it = 0; it < 2; it++) {
+        const int tok = toks[it * 8 + rl];
+        const uint16_t *src = p.qkv + (size_t)(tok < 0 ? 0 : tok) * p.row + (size_t)p.nh * 2 * HD + (size_t)kh * HD + c * 8;
+        kw[it] = tok >= 0 ? *(const u32x4 *)src : u32x4{0, 0, 0, 0};
+        vw[it] = tok >= 0 ? *(const u32x4 *)(src + (size_t)p.nkv * HD) : u32x4{0, 0, 0, 0};
+    }
+    float wn[8];
+    if (p.k_norm) {
+        const float4 w0 = *(const float4 *)(p.k_norm + c * 8), w1 = *(const float4 *)(p.k_norm + c * 8 + 4);
+        wn[0] = w0.x; wn[1] = w0.y; wn[2] = w0.z; wn[3] = w0.w; wn[4] = w1.x; wn[5] = w1.y; wn[6] = w1.z; wn[7] = w1.w;
+    }
+    const int half_rot = p.n_rot / 2;   // 0 or 32: chunks 0-3 pair with chunks 4-7
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+        const int rr = it * 8 + rl;
+        const int tok = toks[rr];
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[2 * j] = bf_lo(kw[it][j]);
+            x[2 * j + 1] = bf_hi(kw[it][j]);
         }
-        // Rotary pair (i, i + half_rot): lanes own 4 consecutive dims, so the partner of lane
-        // L's dims sits in lane L ^ (half_rot / 4) (half_rot is a power of two >= 4 here).
-        const int xo = half_rot / 4;
-        float y[4];
+        if (p.k_norm) {
+            float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; e++) y[e] = __shfl_xor(x[e], xo > 0 ? xo : 1, 64);
-        if (4 * lane < p.n_rot) {
-            const bool first = (4 * lane) < half_rot;
-            const int32_t *pp = p.pos3 + 3 * (size_t)tok;
+            for (int e = 0; e < 8; e++) ss += x[e] * x[e];
+            ss = row16_sum(ss);
+            ss += __shfl_xor(ss, 16, 64);
+            const float inv = rsqrtf(ss / (float)HD + p.eps);
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int i = (4 * lane + e) % half_rot;
-                const float ang = (float)pp[i % 3] * p.inv_freq[i];
-                float sn, cs;
-                sincosf(ang, &sn, &cs);
-                x[e] = first ? x[e] * cs - y[e] * sn : x[e] * cs + y[e] * sn;
+            for (int e = 0; e < 8; e++) x[e] *= inv * wn[e];
+        }
+        if (half_rot) {
+            // partner chunk c ^ 4 (lanes 4 apart inside the 16-lane DPP row)
+            float y[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                // row_ror:n hands lane i the value of lane (i - n) mod 16
+                const float up = __builtin_amdgcn_update_dpp(0.f, x[e], 0x12c, 0xf, 0xf, false);   // lane + 4
+                const float dn = __builtin_amdgcn_update_dpp(0.f, x[e], 0x124, 0xf, 0xf, false);   // lane - 4
+                y[e] = (c & 4) ? dn : up;
+            }
+            if (c < 8 && tok >= 0) {
+                const bool first = c < 4;
+                const int32_t *pp = p.pos3 + 3 * (size_t)tok;
+                float *cs = p.rope_cs ? p.rope_cs + (size_t)tok * 2 * half_rot : nullptr;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int i = (c & 3) * 8 + e;
+                    float sn, cn;
+                    sincosf((float)pp[i % 3] * p.inv_freq[i], &sn, &cn);
+                    x[e] = first ? x[e] * cn - y[e] * sn : x[e] * cn + y[e] * sn;
+                    if (cs && first) *(float2 *)(cs + 2 * i) = make_float2(cn, sn);
+                }
             }
         }
-        const int kvr = row0 + r;
-        u32x2 ko = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])};
-        *(u32x2 *)(p.k_plane + ((size_t)kh * p.kvT + kvr) * HD + 4 * lane) = ko;
-        const uint16_t *vs = src + (size_t)p.nkv * HD;
-        const u32x2 vw = *(const u32x2 *)(vs + 4 * lane);
-        vt[(4 * lane + 0) * (ROWS + 8) + r] = (uint16_t)(vw[0] & 0xffff);
-        vt[(4 * lane + 1) * (ROWS + 8) + r] = (uint16_t)(vw[0] >> 16);
-        vt[(4 * lane + 2) * (ROWS + 8) + r] = (uint16_t)(vw[1] & 0xffff);
-        vt[(4 * lane + 3) * (ROWS + 8) + r] = (uint16_t)(vw[1] >> 16);
+        if (tok >= 0) {
+            u32x4 ko = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7])};
+            *(u32x4 *)(p.k_plane + ((size_t)kh * p.kvT + row0 + rr) * HD + c * 8) = ko;
+        }
+        *(u32x4 *)(vr + rr * VS + c * 8) = vw[it];
     }
     __syncthreads();
-    // V^T rows: HD dims x 64 keys, 16-byte chunks of 8 keys.
-    for (int id = tid; id < HD * (ROWS / 8); id += 256) {
-        const int d = id / (ROWS / 8), c8 = id % (ROWS / 8);
-        uint16_t *dst = p.vt_plane + ((size_t)kh * HD + d) * p.kvT + row0 + c8 * 8;
+    // V^T: HD dims x 16 keys, two 8-key chunks per dim
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int id = tid + 256 * q;
+        const int d = id >> 1, c8 = id & 1;
+        uint16_t v[8];
         bool all = true;
 #pragma unroll
-        for (int e = 0; e < 8; e++) all = all && toks[c8 * 8 + e] >= 0;
+        for (int e = 0; e < 8; e++) {
+            v[e] = vr[(c8 * 8 + e) * VS + d];
+            all = all && toks[c8 * 8 + e] >= 0;
+        }
+        uint16_t *dst = p.vt_plane + ((size_t)kh * HD + d) * p.kvT + row0 + c8 * 8;
         if (all) {
-            *(u32x4 *)dst = *(const u32x4 *)(vt + d * (ROWS + 8) + c8 * 8);
+            u32x4 w = {(unsigned)v[0] | ((unsigned)v[1] << 16), (unsigned)v[2] | ((unsigned)v[3] << 16),
+                       (unsigned)v[4] | ((unsigned)v[5] << 16), (unsigned)v[6] | ((unsigned)v[7] << 16)};
+            *(u32x4 *)dst = w;
         } else {
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                if (toks[c8 * 8 + e] >= 0) dst[e] = vt[d * (ROWS + 8) + c8 * 8 + e];
+                if (toks[c8 * 8 + e] >= 0) dst[e] = v[e];
         }
     }
 }

@@ -11,15 +11,20 @@ struct AttnParams {
     const float *q_norm;
     const int32_t *pos3;
     const float *inv_freq;
+    const float *rope_cs;     // text: cos/sin per pass row [T][n_rot/2][2], or NULL
     const uint16_t *q_plane;  // vision: prepared Q [heads][T][HDK]
     const uint16_t *k_plane;
     const uint16_t *vt_plane;
     const int32_t *blocks;
+    const int32_t *sched;     // work items (block * nh + head) grouped by slot, or NULL
+    const int32_t *sched_off; // [n_slots + 1] item range of each slot
     void *out;
     int32_t *ovf;
     int row, T, kvT, nh, nkv, n_rot;
     float eps, scale_log2, f16_lim;
     int causal, gate, out_type, out_ld;
+    int xcd_heads;            // nh / 8 when heads split evenly over the 8 XCDs, else 0
+    uint64_t *trace;          // NULL, or [grid][4] per-workgroup start, end, HW_ID, XCC_ID
 };
 
 struct PrepParams {
@@ -30,6 +35,7 @@ struct PrepParams {
     const int32_t *kv_tok;
     uint16_t *k_plane;
     uint16_t *vt_plane;
+    float *rope_cs;
     int row, nh, nkv, n_rot, kvT, kv_rows;
     float eps;
 };

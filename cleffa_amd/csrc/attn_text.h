@@ -20,6 +20,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 #include "attn_kernels.h"
 #include "attn_params.h"
 
@@ -47,19 +49,57 @@ __device__ __forceinline__ int s_row_key(int kt, int r) {
 __device__ __forceinline__ int k_swz(int key) { return (key & 15) ^ ((key >> 4) << 2); }
 // XOR swizzle of a V^T row's chunks (rows of 8 chunks, two rows per 256-byte bank line)
 __device__ __forceinline__ int v_swz(int d) { return ((d >> 1) & 1) | (((d >> 3) & 3) << 1); }
+// Sum / max over the four 16-lane rows of a wave (v_permlane16_swap / v_permlane32_swap, VALU
+// only, so no LDS traffic). Every lane gets the same bits.
+__device__ __forceinline__ float xrow_max(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float m = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float xrow_sum(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float m = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+// LDS operand reads issued as ds_read_b128 with an explicit lgkmcnt wait per use. The compiler
+// would otherwise wait for every outstanding LDS access (lgkmcnt(0)) before each use while the
+// global_load_lds fills of the other buffer are in flight. lds_wait ties the wait to the value
+// it guards, so the product that consumes it cannot be scheduled above the wait.
+template <int OFF>
+__device__ __forceinline__ bf16x8 lds_read16(unsigned addr) {
+    bf16x8 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+    return r;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(bf16x8 &r) {
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
+}
+__device__ __forceinline__ unsigned lds_addr(const uint16_t *p) {
+    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) uint16_t *)p;
+}
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 }  // namespace text
 
+// One (query block, q head) work item.
 template <int NROT>
-__global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
+__device__ __forceinline__ void text_block(const AttnParams &p, const int bi, const int h,
+                                           uint16_t *k0s, uint16_t *k1s, uint16_t *v0s, uint16_t *v1s) {
     using namespace text;
     static_assert(NROT % 64 == 0 && NROT <= HD, "rotary pairs must sit in one lane");
-    __shared__ __attribute__((aligned(16))) uint16_t smem[LDS_ELEMS];
-
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int q16 = lane & 15, g = lane >> 4;
 
-    const int bi = blockIdx.x / p.nh;
-    const int h = blockIdx.x - bi * p.nh;
     const int32_t *blk = p.blocks + 8 * bi;
     const int q_row0 = blk[0], nq = blk[1], q_pos0 = blk[2], k_row0 = blk[3], k_len = blk[4];
     const int flag_row = blk[5];
@@ -71,6 +111,70 @@ __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
     const bool wave_live = wave * ROWS < nq;
     const int wave_last_pos = q_pos0 + wave * ROWS + ROWS - 1;
     const size_t qrow = (size_t)q_row0 + (q_valid ? my_q : 0);
+
+    // ---- tiles
+    const uint16_t *kbase = p.k_plane + ((size_t)kh * p.kvT + k_row0) * HD;
+    const uint16_t *vbase = p.vt_plane + (size_t)kh * HD * p.kvT + k_row0;
+    const int last_chunk = ((k_len > 0 ? k_len - 1 : 0) / 8) * 8;
+
+    // Wave w fills slots [(4w + j) * 64, +64) of each 2048-slot tile, one global_load_lds per j.
+    // K slot s: key s/32, chunk (s%32) ^ k_swz(key). V^T slot s: dim s/8, chunk (s%8) ^ v_swz(dim).
+    // Rows past the record are clamped to valid addresses; their scores are masked and their
+    // values zeroed in LDS before use.
+    auto load_tiles = [&](int kb, uint16_t *Ks, uint16_t *Vs) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int grp = wave * 4 + j;
+            const int key = grp * 2 + (lane >> 5);
+            const int c = (lane & 31) ^ k_swz(key);
+            const int krow = min(kb + key, k_len - 1);
+            __builtin_amdgcn_global_load_lds((const void *)(kbase + (size_t)krow * HD + c * 8),
+                                             (lds_void *)(Ks + grp * 512), 16, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int grp = wave * 4 + j;
+            const int d = grp * 8 + (lane >> 3);
+            const int c = (lane & 7) ^ v_swz(d);
+            const int kk = min(kb + c * 8, last_chunk);
+            __builtin_amdgcn_global_load_lds((const void *)(vbase + (size_t)d * p.kvT + kk),
+                                             (lds_void *)(Vs + grp * 512), 16, 0, 0);
+        }
+    };
+    auto zero_tail = [&](int kb, uint16_t *Vs) {   // V^T entries of keys >= k_len -> 0
+        const int valid = k_len - kb;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int s = tid + 512 * j;
+            const int d = s >> 3, c = (s & 7) ^ v_swz(d);
+            const int k0 = c * 8;
+            u32x4 w = *(u32x4 *)(Vs + s * 8);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const unsigned keep = (k0 + 2 * e + 1 < valid) ? 0xffffffffu : (k0 + 2 * e < valid ? 0xffffu : 0u);
+                w[e] &= keep;
+            }
+            *(u32x4 *)(Vs + s * 8) = w;
+        }
+    };
+
+    // per-lane LDS element offsets of the A operands
+    int koff[4][4];   // [S tile kt][c & 3]; chunk 4c + g of key s_row_key(kt, q16)
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+        const int key = s_row_key(kt, q16);
+        const int x = k_swz(key);
+#pragma unroll
+        for (int cl = 0; cl < 4; cl++) koff[kt][cl] = key * HD + (((4 * cl + g) ^ x) * 8);
+    }
+    const int vrow = 8 * (q16 >> 2) + (q16 & 3);   // + 32*(mt>>1) + 4*(mt&1)
+    const int vx = v_swz(vrow);                      // the mt part does not change the swizzle
+    const int voff0 = vrow * BK + ((g ^ vx) * 8);
+    const int voff1 = vrow * BK + (((4 + g) ^ vx) * 8);
+
+    const int n_tiles = (k_len + BK - 1) / BK;
+    // the first tile streams in while the Q prologue runs
+    if (n_tiles > 0) load_tiles(0, k0s, v0s);
 
     // ---- Q prologue: lane holds Q[my_q][c*32 + 8g + j], the B operand of chunk c.
     bf16x8 qf[NC];
@@ -108,6 +212,25 @@ __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
             constexpr int R = NROT / 64;
             const int32_t *pp = p.pos3 + 3 * qrow;
             const float pt = (float)pp[0], ph = (float)pp[1], pw = (float)pp[2];
+            if (p.rope_cs) {   // cos/sin written by the K/V prologue for this pass row
+                const float *cs = p.rope_cs + qrow * (NROT / 2) * 2;
+#pragma unroll
+                for (int c = 0; c < R; c++) {
+                    float t[16];
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++) {
+                        const float4 v = *(const float4 *)(cs + 2 * (c * 32 + 8 * g) + 4 * q4);
+                        t[4 * q4] = v.x; t[4 * q4 + 1] = v.y; t[4 * q4 + 2] = v.z; t[4 * q4 + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const float cs_ = t[2 * j], sn = t[2 * j + 1];
+                        const float x0 = x[c][j], x1 = x[c + R][j];
+                        x[c][j] = x0 * cs_ - x1 * sn;
+                        x[c + R][j] = x1 * cs_ + x0 * sn;
+                    }
+                }
+            } else
 #pragma unroll
             for (int c = 0; c < R; c++) {
                 const float4 f0 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g);
@@ -134,102 +257,60 @@ __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
         }
     }
 
-    // ---- tiles
-    const uint16_t *kbase = p.k_plane + ((size_t)kh * p.kvT + k_row0) * HD;
-    const uint16_t *vbase = p.vt_plane + (size_t)kh * HD * p.kvT + k_row0;
-    const int last_chunk = ((k_len > 0 ? k_len - 1 : 0) / 8) * 8;
-    auto Kbuf = [&](int b) { return smem + b * KTILE; };
-    auto Vbuf = [&](int b) { return smem + 2 * KTILE + b * VTILE; };
-
-    // Wave w fills slots [(4w + j) * 64, +64) of each 2048-slot tile, one global_load_lds per j.
-    // K slot s: key s/32, chunk (s%32) ^ k_swz(key). V^T slot s: dim s/8, chunk (s%8) ^ v_swz(dim).
-    // Rows past the record are clamped to valid addresses; their scores are masked and their
-    // values zeroed in LDS before use.
-    auto load_tiles = [&](int kb, int b) {
-        uint16_t *Ks = Kbuf(b), *Vs = Vbuf(b);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int grp = wave * 4 + j;
-            const int key = grp * 2 + (lane >> 5);
-            const int c = (lane & 31) ^ k_swz(key);
-            const int krow = min(kb + key, k_len - 1);
-            __builtin_amdgcn_global_load_lds((const void *)(kbase + (size_t)krow * HD + c * 8),
-                                             (lds_void *)(Ks + grp * 512), 16, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int grp = wave * 4 + j;
-            const int d = grp * 8 + (lane >> 3);
-            const int c = (lane & 7) ^ v_swz(d);
-            const int kk = min(kb + c * 8, last_chunk);
-            __builtin_amdgcn_global_load_lds((const void *)(vbase + (size_t)d * p.kvT + kk),
-                                             (lds_void *)(Vs + grp * 512), 16, 0, 0);
-        }
-    };
-    auto zero_tail = [&](int kb, int b) {   // V^T entries of keys >= k_len -> 0
-        uint16_t *Vs = Vbuf(b);
-        const int valid = k_len - kb;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int s = tid + 512 * j;
-            const int d = s >> 3, c = (s & 7) ^ v_swz(d);
-            const int k0 = c * 8;
-            u32x4 w = *(u32x4 *)(Vs + s * 8);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const unsigned keep = (k0 + 2 * e + 1 < valid) ? 0xffffffffu : (k0 + 2 * e < valid ? 0xffffu : 0u);
-                w[e] &= keep;
-            }
-            *(u32x4 *)(Vs + s * 8) = w;
-        }
-    };
-
-    // per-lane LDS element offsets of the A operands
-    int koff[4][4];   // [S tile kt][c & 3]; chunk 4c + g of key s_row_key(kt, q16)
-#pragma unroll
-    for (int kt = 0; kt < 4; kt++) {
-        const int key = s_row_key(kt, q16);
-        const int x = k_swz(key);
-#pragma unroll
-        for (int cl = 0; cl < 4; cl++) koff[kt][cl] = key * HD + (((4 * cl + g) ^ x) * 8);
-    }
-    const int vrow = 8 * (q16 >> 2) + (q16 & 3);   // + 32*(mt>>1) + 4*(mt&1)
-    const int vx = v_swz(vrow);                      // the mt part does not change the swizzle
-    const int voff0 = vrow * BK + ((g ^ vx) * 8);
-    const int voff1 = vrow * BK + (((4 + g) ^ vx) * 8);
-
     f32x4 o[16];
 #pragma unroll
     for (int mt = 0; mt < 16; mt++) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;
     const float sl2 = p.scale_log2;
-    const int n_tiles = (k_len + BK - 1) / BK;
-
-    if (n_tiles > 0) {
-        load_tiles(0, 0);
-        __builtin_amdgcn_s_waitcnt(0);
-    }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int t = 0; t < n_tiles; t++) {
+    // The buffers are distinct __shared__ arrays and each use below names one statically, so
+    // the compiler can tell the reads of one buffer from the LDS-DMA writes into the other
+    // and keeps exact lgkmcnt waits.
+    auto tile = [&](const int t, const uint16_t *Ks, const uint16_t *Vs, uint16_t *Kn, uint16_t *Vn) {
         const int kb = t * BK;
-        const int b = t & 1;
         if (kb + BK > k_len) {   // WG-uniform: the block's last tile
-            zero_tail(kb, b);
+            zero_tail(kb, (uint16_t *)Vs);
             __syncthreads();
         }
-        if (t + 1 < n_tiles) load_tiles(kb + BK, b ^ 1);
+        if (t + 1 < n_tiles) load_tiles(kb + BK, Kn, Vn);
         if (wave_live && (!p.causal || kb <= wave_last_pos)) {
-            const uint16_t *Ks = Kbuf(b), *Vs = Vbuf(b);
+            // S^T: 32 MFMAs (4 key tiles x 8 dim chunks). K operands are read DEPTH steps ahead
+            // of their product so the LDS latency overlaps the matrix work.
+            constexpr int DEPTH = 6, QK = 4 * NC;
+            const unsigned kl = lds_addr(Ks), vl = lds_addr(Vs);
+            unsigned ka[4][4];   // byte address of (key tile kt, chunk c & 3); (c >> 2) is an offset
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int cl = 0; cl < 4; cl++) ka[kt][cl] = kl + 2 * koff[kt][cl];
             f32x4 s[4];
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++) {
-                s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int c = 0; c < NC; c++) {
-                    const bf16x8 a = *(const bf16x8 *)(Ks + koff[kt][c & 3] + (c >> 2) * 128);
-                    s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[kt], 0, 0, 0);
+            bf16x8 ring[DEPTH];
+            static_for<DEPTH>([&](auto I) {
+                constexpr int st = decltype(I)::value, kt = st / NC, c = st % NC;
+                ring[st] = lds_read16<(c >> 2) * 256>(ka[kt][c & 3]);
+            });
+            static_for<QK>([&](auto I) {
+                constexpr int st = decltype(I)::value, kt = st / NC, c = st % NC;
+                constexpr int ahead = (QK - 1 - st) < (DEPTH - 1) ? (QK - 1 - st) : (DEPTH - 1);
+                bf16x8 a = ring[st % DEPTH];
+                lds_wait<ahead>(a);
+                if constexpr (c == 0) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[kt], 0, 0, 0);
+                if constexpr (st + DEPTH < QK) {
+                    constexpr int n = st + DEPTH, nkt = n / NC, nc = n % NC;
+                    ring[st % DEPTH] = lds_read16<(nc >> 2) * 256>(ka[nkt][nc & 3]);
                 }
-            }
+            });
+            // first V operands, in flight during the softmax
+            const unsigned va0 = vl + 2 * voff0, va1 = vl + 2 * voff1;
+            auto vread = [&](auto I) {   // step st = 2 * mt + kc
+                constexpr int st = decltype(I)::value, mt = st >> 1, kc = st & 1;
+                constexpr int off = (32 * (mt >> 1) + 4 * (mt & 1)) * BK * 2;
+                return lds_read16<off>(kc ? va1 : va0);
+            };
+            bf16x8 vring[DEPTH];
+            static_for<DEPTH>([&](auto I) { vring[decltype(I)::value] = vread(I); });
             // Online softmax in the exp2 domain. Masked scores are -inf, so their P is an exact
             // zero and a tile past a row's diagonal rescales the row by exactly 1.
             if ((kb + BK > k_len) || (p.causal && kb + BK - 1 > q_pos0 + wave * ROWS)) {
@@ -246,8 +327,7 @@ __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kt][i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+            mx = xrow_max(mx) * sl2;
             const float mn = fmaxf(m_run, mx);
             const float msub = (mn == -INFINITY) ? 0.f : mn;
             const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
@@ -269,25 +349,28 @@ __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
                 u32x4 wv = {w[0], w[1], w[2], w[3]};
                 pk[kc] = __builtin_bit_cast(bf16x8, wv);
             }
-            rs += __shfl_xor(rs, 16, 64);
-            rs += __shfl_xor(rs, 32, 64);
+            rs = xrow_sum(rs);
             l_run = l_run * alpha + rs;
             m_run = mn;
             if (__any(alpha != 1.f)) {
 #pragma unroll
                 for (int mt = 0; mt < 16; mt++) o[mt] *= alpha;
             }
-#pragma unroll
-            for (int mt = 0; mt < 16; mt++) {
-                const int base = (32 * (mt >> 1) + 4 * (mt & 1)) * BK;
-                const bf16x8 a0 = *(const bf16x8 *)(Vs + base + voff0);
-                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, pk[0], o[mt], 0, 0, 0);
-                const bf16x8 a1 = *(const bf16x8 *)(Vs + base + voff1);
-                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, pk[1], o[mt], 0, 0, 0);
-            }
+            static_for<32>([&](auto I) {   // O^T: 32 MFMAs, same read-ahead
+                constexpr int st = decltype(I)::value, mt = st >> 1, kc = st & 1;
+                constexpr int ahead = (31 - st) < (DEPTH - 1) ? (31 - st) : (DEPTH - 1);
+                bf16x8 a = vring[st % DEPTH];
+                lds_wait<ahead>(a);
+                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[kc], o[mt], 0, 0, 0);
+                if constexpr (st + DEPTH < 32) vring[st % DEPTH] = vread(std::integral_constant<int, st + DEPTH>{});
+            });
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+        tile(t, k0s, v0s, k1s, v1s);
+        if (t + 1 < n_tiles) tile(t + 1, k1s, v1s, k0s, v0s);
     }
 
     // ---- Epilogue: O / l times sigmoid(gate); lane (q16, g) holds dims 32u + 8g + [0, 8).
@@ -314,6 +397,55 @@ __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
             }
             store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);
         }
+    }
+}
+
+// Grid: one workgroup per work item (blockIdx = block * nh + head), or, with a schedule, one
+// persistent workgroup per slot that runs its items in order (the host balances the slots).
+template <int NROT>
+__global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t k0s[text::KTILE];
+    __shared__ __attribute__((aligned(16))) uint16_t k1s[text::KTILE];
+    __shared__ __attribute__((aligned(16))) uint16_t v0s[text::VTILE];
+    __shared__ __attribute__((aligned(16))) uint16_t v1s[text::VTILE];
+    uint64_t t0 = 0;
+    if (p.trace && threadIdx.x == 0) t0 = wall_clock64();
+    // Work items: one per workgroup (blockIdx = block * nh + head, or the XCD-grouped order),
+    // or with a schedule the slot's list, run in order by one persistent workgroup.
+    int w0 = 0, w1 = 1;
+    if (p.sched) {
+        w0 = p.sched_off[blockIdx.x];
+        w1 = p.sched_off[blockIdx.x + 1];
+    }
+    for (int w = w0; w < w1; w++) {
+        int bi, h;
+        if (p.sched) {
+            const int item = p.sched[w];
+            bi = item / p.nh;
+            h = item - bi * p.nh;
+        } else if (p.xcd_heads) {
+            // Workgroup ids go round-robin over the 8 XCDs (each with its own L2). XCD x takes
+            // heads x*xcd_heads .. +xcd_heads-1 of every block, so it streams the K/V of as few
+            // KV heads as possible; blocks stay in the plan's longest-first order.
+            const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+            bi = j / p.xcd_heads;
+            h = x * p.xcd_heads + (j - bi * p.xcd_heads);
+        } else {
+            bi = blockIdx.x / p.nh;
+            h = blockIdx.x - bi * p.nh;
+        }
+        if (w > w0) __syncthreads();   // the next item reuses the LDS tiles
+        text_block<NROT>(p, bi, h, k0s, k1s, v0s, v1s);
+    }
+    if (p.trace && threadIdx.x == 0) {
+        // per-workgroup trace: start / end (100 MHz wall clock), hardware id, XCC id
+        const uint64_t t1 = wall_clock64();
+        const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+        const unsigned xcc = __builtin_amdgcn_s_getreg((15 << 11) | 20);
+        p.trace[4 * blockIdx.x] = t0;
+        p.trace[4 * blockIdx.x + 1] = t1;
+        p.trace[4 * blockIdx.x + 2] = hw;
+        p.trace[4 * blockIdx.x + 3] = xcc;
     }
 }
 
