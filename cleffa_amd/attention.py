@@ -129,24 +129,6 @@ class AttnPlan:
         # kv rows the planes must hold, rounded to the 16-byte V^T chunk
         self.kvT = max(8, (self.kv_rows + 7) // 8 * 8)
 
-    def schedule(self, nh, n_slots):
-        """Persistent-workgroup schedule of this plan's (block, head) items over n_slots slots
-        (host-built, cached per (nh, n_slots)); returns (items, slot_off) device tensors."""
-        key = (nh, n_slots)
-        if not hasattr(self, "_sched"):
-            self._sched = {}
-        if key not in self._sched:
-            lib = _lib.load()
-            items = np.zeros(max(self.n_blk * nh, 1), dtype=np.int32)
-            off = np.zeros(n_slots + 1, dtype=np.int32)
-            err = _err()
-            blocks = np.ascontiguousarray(self.blocks_host if self.n_blk else np.zeros((1, BLOCK_INTS), np.int32))
-            _lib.check(lib.clef_hip_attn_schedule(_i32p(blocks), self.n_blk, nh, n_slots, _i32p(items),
-                                                  _i32p(off), err, len(err)), err)
-            self._sched[key] = (items[: self.n_blk * nh].copy(), off.copy(),
-                                torch.from_numpy(items).to(self.device), torch.from_numpy(off).to(self.device))
-        return self._sched[key]
-
     def pairs(self):
         """(query, key) pairs the plan visits under its mask: the algorithmic work unit."""
         total = 0
@@ -176,16 +158,12 @@ def _check(t, name, shape, dtype, device):
 class TextAttention:
     """One gated full-attention layer of the dense Clef models (hd 256, GQA)."""
 
-    def __init__(self, nh, nkv, hd=256, n_rot=64, eps=1e-6, rope_theta=1e7, device="cuda",
-                 persistent=False):
-        """persistent: run the attention kernel as one workgroup per compute unit over a
-        host-balanced schedule (False: one workgroup per (block, head) item)."""
+    def __init__(self, nh, nkv, hd=256, n_rot=64, eps=1e-6, rope_theta=1e7, device="cuda"):
         self.nh, self.nkv, self.hd, self.n_rot, self.eps = nh, nkv, hd, n_rot, eps
         self.scale = 1.0 / math.sqrt(hd)
         self.row = 2 * nh * hd + 2 * nkv * hd
         self.device = _device(device)
         init_device(self.device)
-        self.slots = torch.cuda.get_device_properties(self.device).multi_processor_count if persistent else 0
         self.inv_freq = torch.from_numpy(rope_inv_freq(rope_theta, n_rot).copy()).to(self.device) \
             if n_rot else torch.zeros(1, dtype=torch.float32, device=self.device)
 
@@ -237,9 +215,6 @@ class TextAttention:
         a.pos3, a.inv_freq, a.rope_cs = _ptr(pos3), _ptr(self.inv_freq), _ptr(rope_cs)
         a.k_plane, a.vt_plane, a.kvT = _ptr(k_plane), _ptr(vt_plane), kvT
         a.blocks, a.n_blk = _ptr(plan.blocks), plan.n_blk
-        if self.slots > 0 and plan.n_blk:
-            _, _, items, off = plan.schedule(self.nh, self.slots)
-            a.sched, a.sched_off, a.n_slots = _ptr(items), _ptr(off), self.slots
         a.kv_tok, a.kv_rows = _ptr(plan.kv_tok), plan.kv_rows
         a.causal, a.gate = int(plan.causal), int(gate)
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)

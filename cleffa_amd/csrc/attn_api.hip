@@ -163,51 +163,6 @@ bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int
     return true;
 }
 
-bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int n_slots, int32_t *items,
-                            int32_t *slot_off, char *err, size_t errlen) {
-    if (n_blk < 0 || nh <= 0 || n_slots <= 0 || (n_blk && (!blocks || !items)) || !slot_off)
-        return fail(err, errlen, "bad schedule arguments");
-    const long n_items = (long)n_blk * nh;
-    if (n_items > 0x7fffffffL) return fail(err, errlen, "too many work items");
-    struct It { int cost, id; };
-    std::vector<It> its((size_t)n_items);
-    for (int b = 0; b < n_blk; b++) {
-        const int cost = (blocks[CLEF_HIP_BLOCK_INTS * b + 4] + 63) / 64 + 2;
-        for (int h = 0; h < nh; h++) its[(size_t)b * nh + h] = {cost, b * nh + h};
-    }
-    std::stable_sort(its.begin(), its.end(), [](const It &x, const It &y) { return x.cost > y.cost; });
-    // greedy: each item to the least loaded slot (ties: lowest slot)
-    std::vector<long> load((size_t)n_slots, 0);
-    std::vector<std::vector<int>> lists((size_t)n_slots);
-    std::vector<std::pair<long, int>> heap;
-    for (int s = 0; s < n_slots; s++) heap.push_back({0L, s});
-    auto cmp = [](const std::pair<long, int> &x, const std::pair<long, int> &y) {
-        return x.first != y.first ? x.first > y.first : x.second > y.second;
-    };
-    std::make_heap(heap.begin(), heap.end(), cmp);
-    for (const It &it : its) {
-        std::pop_heap(heap.begin(), heap.end(), cmp);
-        auto &top = heap.back();
-        lists[(size_t)top.second].push_back(it.id);
-        top.first += it.cost;
-        std::push_heap(heap.begin(), heap.end(), cmp);
-    }
-    int k = 0;
-    for (int s = 0; s < n_slots; s++) {
-        slot_off[s] = k;
-        for (int id : lists[(size_t)s]) items[k++] = id;
-    }
-    slot_off[n_slots] = k;
-    return true;
-}
-
-int clef_hip_attn_device_slots(void) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return -1;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
-    return n;
-}
-
 void clef_hip_rope_inv_freq(float theta, int n_rot, float *inv_freq) {
     for (int j = 0; j < n_rot / 2; j++) inv_freq[j] = 1.0f / powf(theta, (float)(2 * j) / (float)n_rot);
 }
@@ -249,7 +204,6 @@ bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, si
     p.qkv = a->qkv; p.q_norm = a->q_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
     p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
     p.k_plane = a->k_plane; p.vt_plane = a->vt_plane; p.blocks = a->blocks;
-    p.sched = a->n_slots > 0 ? a->sched : nullptr; p.sched_off = a->sched_off;
     p.out = a->out; p.ovf = a->ovf;
     p.row = a->row; p.T = a->T; p.kvT = a->kvT; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot;
     p.eps = a->eps; p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = a->f16_lim;
@@ -257,8 +211,7 @@ bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, si
     p.out_ld = a->nh * a->hd;
     p.trace = a->trace;
     p.xcd_heads = (a->nh % 8 == 0 && (a->nh / 8) > 0 && ((a->nh / a->nkv) % (a->nh / 8) == 0 || (a->nh / 8) % (a->nh / a->nkv) == 0)) ? a->nh / 8 : 0;
-    if (a->n_slots > 0 && (!a->sched || !a->sched_off)) return fail(err, errlen, "missing schedule");
-    const long grid = a->n_slots > 0 ? (long)a->n_slots : (long)a->n_blk * a->nh;
+    const long grid = (long)a->n_blk * a->nh;
     if (grid > 0x7fffffffL) return fail(err, errlen, "grid too large");
     if (a->n_rot == 64)
         hipLaunchKernelGGL(attn_text_kernel<64>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);

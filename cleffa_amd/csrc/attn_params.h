@@ -16,8 +16,6 @@ struct AttnParams {
     const uint16_t *k_plane;
     const uint16_t *vt_plane;
     const int32_t *blocks;
-    const int32_t *sched;     // work items (block * nh + head) grouped by slot, or NULL
-    const int32_t *sched_off; // [n_slots + 1] item range of each slot
     void *out;
     int32_t *ovf;
     int row, T, kvT, nh, nkv, n_rot;

@@ -94,7 +94,7 @@ __device__ __forceinline__ void static_for(F &&f) {
 // One (query block, q head) work item.
 template <int NROT>
 __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, const int h,
-                                           uint16_t *k0s, uint16_t *k1s, uint16_t *v0s, uint16_t *v1s) {
+                                           uint16_t *smem) {
     using namespace text;
     static_assert(NROT % 64 == 0 && NROT <= HD, "rotary pairs must sit in one lane");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -121,6 +121,10 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     // K slot s: key s/32, chunk (s%32) ^ k_swz(key). V^T slot s: dim s/8, chunk (s%8) ^ v_swz(dim).
     // Rows past the record are clamped to valid addresses; their scores are masked and their
     // values zeroed in LDS before use.
+    // LDS: K0 | K1 | V0 | V1 (32 KB each). Operand reads address K buffers from the LDS base and
+    // V buffers from base + 64 KB, so the buffer choice is an immediate offset.
+    uint16_t *const k0s = smem, *const k1s = smem + KTILE, *const v0s = smem + 2 * KTILE,
+                   *const v1s = smem + 2 * KTILE + VTILE;
     auto load_tiles = [&](int kb, uint16_t *Ks, uint16_t *Vs) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -141,6 +145,21 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
                                              (lds_void *)(Vs + grp * 512), 16, 0, 0);
         }
     };
+    // Gate rows of the block (128 x 256 bf16 = 64 KB): rows 0-63 into G0, 64-127 into G1, slot
+    // s of a half = row s/32, 16-byte chunk (s%32) ^ (row & 15).
+    auto load_gate = [&](uint16_t *G0, uint16_t *G1) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int grp = wave * 8 + j;   // 64-slot group, 0..63
+            const int row = grp * 2 + (lane >> 5);
+            const int c = (lane & 31) ^ (row & 15);
+            int rc = min(row, nq - 1);
+            asm volatile("" : "+v"(rc));   // keeps the address math here, not hoisted out of the tile loop
+            uint16_t *dst = (grp < 32 ? G0 : G1) + (grp & 31) * 512;
+            __builtin_amdgcn_global_load_lds((const void *)(p.qkv + ((size_t)q_row0 + rc) * p.row + (size_t)h * 2 * HD + HD + c * 8),
+                                             (lds_void *)dst, 16, 0, 0);
+        }
+    };
     auto zero_tail = [&](int kb, uint16_t *Vs) {   // V^T entries of keys >= k_len -> 0
         const int valid = k_len - kb;
 #pragma unroll
@@ -159,18 +178,19 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     };
 
     // per-lane LDS element offsets of the A operands
-    int koff[4][4];   // [S tile kt][c & 3]; chunk 4c + g of key s_row_key(kt, q16)
+    const unsigned kl = lds_addr(smem), vl = kl + 2 * 2 * KTILE;
+    unsigned ka[4][4];   // byte address of (S tile kt, chunk c & 3) in K0; c >> 2 and K1 are offsets
 #pragma unroll
     for (int kt = 0; kt < 4; kt++) {
         const int key = s_row_key(kt, q16);
         const int x = k_swz(key);
 #pragma unroll
-        for (int cl = 0; cl < 4; cl++) koff[kt][cl] = key * HD + (((4 * cl + g) ^ x) * 8);
+        for (int cl = 0; cl < 4; cl++) ka[kt][cl] = kl + 2 * (key * HD + (((4 * cl + g) ^ x) * 8));
     }
     const int vrow = 8 * (q16 >> 2) + (q16 & 3);   // + 32*(mt>>1) + 4*(mt&1)
     const int vx = v_swz(vrow);                      // the mt part does not change the swizzle
-    const int voff0 = vrow * BK + ((g ^ vx) * 8);
-    const int voff1 = vrow * BK + (((4 + g) ^ vx) * 8);
+    const unsigned va0 = vl + 2 * (vrow * BK + ((g ^ vx) * 8));
+    const unsigned va1 = vl + 2 * (vrow * BK + (((4 + g) ^ vx) * 8));
 
     const int n_tiles = (k_len + BK - 1) / BK;
     // the first tile streams in while the Q prologue runs
@@ -179,29 +199,47 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     // ---- Q prologue: lane holds Q[my_q][c*32 + 8g + j], the B operand of chunk c.
     bf16x8 qf[NC];
     {
-        float x[NC][8];
+        // every prologue load is issued before any of them is waited for
         const uint16_t *src = p.qkv + qrow * p.row + (size_t)h * 2 * HD;
+        u32x4 qw[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) qw[c] = q_valid ? *(const u32x4 *)(src + c * 32 + 8 * g) : u32x4{0, 0, 0, 0};
+        float4 wv[NC][2];
+        if (p.q_norm) {   // NULL: no q/k norm (plain SDPA operands)
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                wv[c][0] = *(const float4 *)(p.q_norm + c * 32 + 8 * g);
+                wv[c][1] = *(const float4 *)(p.q_norm + c * 32 + 8 * g + 4);
+            }
+        }
+        constexpr int R = NROT / 64;
+        float4 csv[R > 0 ? R : 1][4];
+        if (NROT > 0 && p.rope_cs) {   // cos/sin written by the K/V prologue for this pass row
+            const float *cs = p.rope_cs + qrow * (NROT / 2) * 2;
+#pragma unroll
+            for (int c = 0; c < R; c++)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++) csv[c][q4] = *(const float4 *)(cs + 2 * (c * 32 + 8 * g) + 4 * q4);
+        }
+        float x[NC][8];
         float ss = 0.f;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            u32x4 w = q_valid ? *(const u32x4 *)(src + c * 32 + 8 * g) : u32x4{0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                x[c][2 * j] = bf_lo(w[j]);
-                x[c][2 * j + 1] = bf_hi(w[j]);
+                x[c][2 * j] = bf_lo(qw[c][j]);
+                x[c][2 * j + 1] = bf_hi(qw[c][j]);
             }
 #pragma unroll
             for (int j = 0; j < 8; j++) ss += x[c][j] * x[c][j];
         }
-        ss += __shfl_xor(ss, 16, 64);
-        ss += __shfl_xor(ss, 32, 64);
-        if (p.q_norm) {   // NULL: no q/k norm (plain SDPA operands)
+        ss = xrow_sum(ss);
+        if (p.q_norm) {
             const float inv = rsqrtf(ss / (float)HD + p.eps);
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                const float4 w0 = *(const float4 *)(p.q_norm + c * 32 + 8 * g);
-                const float4 w1 = *(const float4 *)(p.q_norm + c * 32 + 8 * g + 4);
-                const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                const float wn[8] = {wv[c][0].x, wv[c][0].y, wv[c][0].z, wv[c][0].w,
+                                     wv[c][1].x, wv[c][1].y, wv[c][1].z, wv[c][1].w};
 #pragma unroll
                 for (int j = 0; j < 8; j++) x[c][j] = x[c][j] * inv * wn[j];
             }
@@ -209,19 +247,13 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
         if (NROT > 0) {
             // NeoX partial rotary: pair (i, i + NROT/2) sits in this lane at chunks c and c + R.
             // Interleaved M-RoPE: pair i turns by axis i % 3 of pos3.
-            constexpr int R = NROT / 64;
-            const int32_t *pp = p.pos3 + 3 * qrow;
-            const float pt = (float)pp[0], ph = (float)pp[1], pw = (float)pp[2];
-            if (p.rope_cs) {   // cos/sin written by the K/V prologue for this pass row
-                const float *cs = p.rope_cs + qrow * (NROT / 2) * 2;
+            if (p.rope_cs) {
 #pragma unroll
                 for (int c = 0; c < R; c++) {
-                    float t[16];
-#pragma unroll
-                    for (int q4 = 0; q4 < 4; q4++) {
-                        const float4 v = *(const float4 *)(cs + 2 * (c * 32 + 8 * g) + 4 * q4);
-                        t[4 * q4] = v.x; t[4 * q4 + 1] = v.y; t[4 * q4 + 2] = v.z; t[4 * q4 + 3] = v.w;
-                    }
+                    const float t[16] = {csv[c][0].x, csv[c][0].y, csv[c][0].z, csv[c][0].w,
+                                         csv[c][1].x, csv[c][1].y, csv[c][1].z, csv[c][1].w,
+                                         csv[c][2].x, csv[c][2].y, csv[c][2].z, csv[c][2].w,
+                                         csv[c][3].x, csv[c][3].y, csv[c][3].z, csv[c][3].w};
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
                         const float cs_ = t[2 * j], sn = t[2 * j + 1];
@@ -230,22 +262,25 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
                         x[c + R][j] = x1 * cs_ + x0 * sn;
                     }
                 }
-            } else
+            } else {
+                const int32_t *pp = p.pos3 + 3 * qrow;
+                const float pt = (float)pp[0], ph = (float)pp[1], pw = (float)pp[2];
 #pragma unroll
-            for (int c = 0; c < R; c++) {
-                const float4 f0 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g);
-                const float4 f1 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g + 4);
-                const float fr[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+                for (int c = 0; c < R; c++) {
+                    const float4 f0 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g);
+                    const float4 f1 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g + 4);
+                    const float fr[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const int i = c * 32 + 8 * g + j;
-                    const int ax = i % 3;
-                    const float pos = ax == 0 ? pt : (ax == 1 ? ph : pw);
-                    float sn, cs;
-                    sincosf(pos * fr[j], &sn, &cs);
-                    const float x0 = x[c][j], x1 = x[c + R][j];
-                    x[c][j] = x0 * cs - x1 * sn;
-                    x[c + R][j] = x1 * cs + x0 * sn;
+                    for (int j = 0; j < 8; j++) {
+                        const int i = c * 32 + 8 * g + j;
+                        const int ax = i % 3;
+                        const float pos = ax == 0 ? pt : (ax == 1 ? ph : pw);
+                        float sn, cs;
+                        sincosf(pos * fr[j], &sn, &cs);
+                        const float x0 = x[c][j], x1 = x[c + R][j];
+                        x[c][j] = x0 * cs - x1 * sn;
+                        x[c + R][j] = x1 * cs + x0 * sn;
+                    }
                 }
             }
         }
@@ -264,31 +299,26 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     const float sl2 = p.scale_log2;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    // The buffers are distinct __shared__ arrays and each use below names one statically, so
-    // the compiler can tell the reads of one buffer from the LDS-DMA writes into the other
-    // and keeps exact lgkmcnt waits.
-    auto tile = [&](const int t, const uint16_t *Ks, const uint16_t *Vs, uint16_t *Kn, uint16_t *Vn) {
+    // Two tiles per trip: each call names its read and fill buffers statically.
+    auto tile = [&](const int t, auto BUF) {
+        constexpr int buf = decltype(BUF)::value;
+        uint16_t *const Vs = buf ? v1s : v0s, *const Kn = buf ? k0s : k1s, *const Vn = buf ? v0s : v1s;
         const int kb = t * BK;
         if (kb + BK > k_len) {   // WG-uniform: the block's last tile
-            zero_tail(kb, (uint16_t *)Vs);
+            zero_tail(kb, Vs);
             __syncthreads();
         }
         if (t + 1 < n_tiles) load_tiles(kb + BK, Kn, Vn);
+        else if (p.gate) load_gate(Kn, Vn);   // the idle buffers take the epilogue's gate rows
         if (wave_live && (!p.causal || kb <= wave_last_pos)) {
             // S^T: 32 MFMAs (4 key tiles x 8 dim chunks). K operands are read DEPTH steps ahead
             // of their product so the LDS latency overlaps the matrix work.
             constexpr int DEPTH = 6, QK = 4 * NC;
-            const unsigned kl = lds_addr(Ks), vl = lds_addr(Vs);
-            unsigned ka[4][4];   // byte address of (key tile kt, chunk c & 3); (c >> 2) is an offset
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (int cl = 0; cl < 4; cl++) ka[kt][cl] = kl + 2 * koff[kt][cl];
             f32x4 s[4];
             bf16x8 ring[DEPTH];
             static_for<DEPTH>([&](auto I) {
                 constexpr int st = decltype(I)::value, kt = st / NC, c = st % NC;
-                ring[st] = lds_read16<(c >> 2) * 256>(ka[kt][c & 3]);
+                ring[st] = lds_read16<buf * 2 * KTILE + (c >> 2) * 256>(ka[kt][c & 3]);
             });
             static_for<QK>([&](auto I) {
                 constexpr int st = decltype(I)::value, kt = st / NC, c = st % NC;
@@ -299,14 +329,13 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
                 s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[kt], 0, 0, 0);
                 if constexpr (st + DEPTH < QK) {
                     constexpr int n = st + DEPTH, nkt = n / NC, nc = n % NC;
-                    ring[st % DEPTH] = lds_read16<(nc >> 2) * 256>(ka[nkt][nc & 3]);
+                    ring[st % DEPTH] = lds_read16<buf * 2 * KTILE + (nc >> 2) * 256>(ka[nkt][nc & 3]);
                 }
             });
             // first V operands, in flight during the softmax
-            const unsigned va0 = vl + 2 * voff0, va1 = vl + 2 * voff1;
             auto vread = [&](auto I) {   // step st = 2 * mt + kc
                 constexpr int st = decltype(I)::value, mt = st >> 1, kc = st & 1;
-                constexpr int off = (32 * (mt >> 1) + 4 * (mt & 1)) * BK * 2;
+                constexpr int off = buf * 2 * VTILE + (32 * (mt >> 1) + 4 * (mt & 1)) * BK * 2;
                 return lds_read16<off>(kc ? va1 : va0);
             };
             bf16x8 vring[DEPTH];
@@ -369,11 +398,13 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
         __syncthreads();
     };
     for (int t = 0; t < n_tiles; t += 2) {
-        tile(t, k0s, v0s, k1s, v1s);
-        if (t + 1 < n_tiles) tile(t + 1, k1s, v1s, k0s, v0s);
+        tile(t, std::integral_constant<int, 0>{});
+        if (t + 1 < n_tiles) tile(t + 1, std::integral_constant<int, 1>{});
     }
 
     // ---- Epilogue: O / l times sigmoid(gate); lane (q16, g) holds dims 32u + 8g + [0, 8).
+    // The gate rows were loaded into the buffers the last tile left idle.
+    const uint16_t *gate0 = (n_tiles & 1) ? k1s : k0s, *gate1 = (n_tiles & 1) ? v1s : v0s;
     if (q_valid) {
         const float il = l_run > 0.f ? 1.f / l_run : 0.f;
         const size_t t = (size_t)q_row0 + my_q;
@@ -388,7 +419,9 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
                 v[4 + i] = o[2 * u + 1][i] * il;
             }
             if (p.gate) {
-                const u32x4 gw = *(const u32x4 *)(p.qkv + t * p.row + (size_t)h * 2 * HD + HD + d0);
+                const int c = (4 * u + g) ^ (my_q & 15);
+                const uint16_t *grow = (my_q < 64 ? gate0 : gate1) + (my_q & 63) * 256;
+                const u32x4 gw = *(const u32x4 *)(grow + c * 8);
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     v[2 * j] *= sigmoidf(bf_lo(gw[j]));
@@ -400,43 +433,25 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     }
 }
 
-// Grid: one workgroup per work item (blockIdx = block * nh + head), or, with a schedule, one
-// persistent workgroup per slot that runs its items in order (the host balances the slots).
+// Grid: one workgroup per (query block, q head) work item.
 template <int NROT>
 __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
-    __shared__ __attribute__((aligned(16))) uint16_t k0s[text::KTILE];
-    __shared__ __attribute__((aligned(16))) uint16_t k1s[text::KTILE];
-    __shared__ __attribute__((aligned(16))) uint16_t v0s[text::VTILE];
-    __shared__ __attribute__((aligned(16))) uint16_t v1s[text::VTILE];
+    __shared__ __attribute__((aligned(16))) uint16_t smem[text::LDS_ELEMS];
     uint64_t t0 = 0;
     if (p.trace && threadIdx.x == 0) t0 = wall_clock64();
-    // Work items: one per workgroup (blockIdx = block * nh + head, or the XCD-grouped order),
-    // or with a schedule the slot's list, run in order by one persistent workgroup.
-    int w0 = 0, w1 = 1;
-    if (p.sched) {
-        w0 = p.sched_off[blockIdx.x];
-        w1 = p.sched_off[blockIdx.x + 1];
+    int bi, h;
+    if (p.xcd_heads) {
+        // Workgroup ids go round-robin over the 8 XCDs (each with its own L2). XCD x takes heads
+        // x*xcd_heads .. +xcd_heads-1 of every block, so it streams the K/V of as few KV heads
+        // as possible; blocks stay in the plan's longest-first order.
+        const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+        bi = j / p.xcd_heads;
+        h = x * p.xcd_heads + (j - bi * p.xcd_heads);
+    } else {
+        bi = blockIdx.x / p.nh;
+        h = blockIdx.x - bi * p.nh;
     }
-    for (int w = w0; w < w1; w++) {
-        int bi, h;
-        if (p.sched) {
-            const int item = p.sched[w];
-            bi = item / p.nh;
-            h = item - bi * p.nh;
-        } else if (p.xcd_heads) {
-            // Workgroup ids go round-robin over the 8 XCDs (each with its own L2). XCD x takes
-            // heads x*xcd_heads .. +xcd_heads-1 of every block, so it streams the K/V of as few
-            // KV heads as possible; blocks stay in the plan's longest-first order.
-            const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
-            bi = j / p.xcd_heads;
-            h = x * p.xcd_heads + (j - bi * p.xcd_heads);
-        } else {
-            bi = blockIdx.x / p.nh;
-            h = blockIdx.x - bi * p.nh;
-        }
-        if (w > w0) __syncthreads();   // the next item reuses the LDS tiles
-        text_block<NROT>(p, bi, h, k0s, k1s, v0s, v1s);
-    }
+    text_block<NROT>(p, bi, h, smem);
     if (p.trace && threadIdx.x == 0) {
         // per-workgroup trace: start / end (100 MHz wall clock), hardware id, XCC id
         const uint64_t t1 = wall_clock64();

@@ -73,16 +73,6 @@ bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int
                         int32_t *blocks, int max_blocks, int32_t *kv_tok, int max_kv,
                         int *n_blk, int *kv_rows, char *err, size_t errlen);
 
-/* Host-only: balances the (query block, q head) work items of a plan over n_slots persistent
- * workgroups (one per CU: clef_hip_attn_device_slots). Longest-processing-time-first greedy on
- * the cost ceil(k_len/64) + 2 per item. items [n_blk*nh] receive block*nh + head grouped by
- * slot, slot_off [n_slots+1] each slot's range. Reproduces nothing in the reference, whose
- * GPU dispatches one threadgroup per item (clef_metal.m:869-880); results do not depend on it. */
-bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int n_slots, int32_t *items,
-                            int32_t *slot_off, char *err, size_t errlen);
-/* Compute units of the current device (the slot count for clef_hip_attn_schedule), or -1. */
-int clef_hip_attn_device_slots(void);
-
 /* RoPE frequency table: inv_freq[j] = 1 / theta^(2j/n_rot) in f32, j < n_rot/2
  * (clef_metal.m:176-184 text, 186-192 vision with n_rot = hd/2 and theta = 10000). */
 void clef_hip_rope_inv_freq(float theta, int n_rot, float *inv_freq);
@@ -111,10 +101,6 @@ typedef struct {
     int kvT;                  /* rows per head of the planes: >= plan kv_rows, multiple of 8 */
     const int32_t *blocks;    /* device copy of the plan's blocks */
     int n_blk;
-    const int32_t *sched;     /* device copy of clef_hip_attn_schedule items, or NULL: one
-                                 workgroup per item */
-    const int32_t *sched_off; /* device copy of its slot_off */
-    int n_slots;
     const int32_t *kv_tok;    /* device copy of the plan's kv_tok */
     int kv_rows;
     int causal;               /* 1 for the text models */
