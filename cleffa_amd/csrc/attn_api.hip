@@ -57,6 +57,7 @@ bool check_text(const clef_hip_attn_args *a, bool need_core, char *err, size_t e
     const long need_row = 2L * a->nh * a->hd + 2L * a->nkv * a->hd;
     if (a->row < need_row || a->row % 8) return fail(err, errlen, "qkv row %d must be >= %ld and a multiple of 8", a->row, need_row);
     if (a->kvT % 8 || a->kvT < a->kv_rows) return fail(err, errlen, "kvT %d must be a multiple of 8 and >= kv_rows %d", a->kvT, a->kv_rows);
+    if ((long)a->kvT * a->hd * 2 >= (1L << 32)) return fail(err, errlen, "kvT %d too large for 32-bit plane offsets", a->kvT);
     if (!a->qkv || !aligned16(a->qkv)) return fail(err, errlen, "qkv must be a 16-byte aligned device pointer");
     if (!aligned16(a->k_norm) || !aligned16(a->q_norm)) return fail(err, errlen, "norm weights must be 16-byte aligned");
     if (!a->k_norm != !a->q_norm) return fail(err, errlen, "q_norm and k_norm must both be set or both be NULL");
@@ -141,7 +142,16 @@ bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int
             ents.push_back(e);
         }
     }
-    const int total_kv = cu_k ? cu_k[n_seq] : kv_off;
+    // rows per head the planes need: the fills read whole 64-key tiles from each record's first key
+    int total_kv = 0;
+    kv_off = 0;
+    for (int r = 0; r < n_seq; r++) {
+        const int nq = cu_q[r + 1] - cu_q[r];
+        const int nk = cu_k ? cu_k[r + 1] - cu_k[r] : nq;
+        const int k0 = cu_k ? cu_k[r] : kv_off;
+        total_kv = std::max(total_kv, k0 + (nk + CLEF_HIP_KV_ALIGN - 1) / CLEF_HIP_KV_ALIGN * CLEF_HIP_KV_ALIGN);
+        if (!cu_k) kv_off += (nq + CLEF_HIP_KV_ALIGN - 1) / CLEF_HIP_KV_ALIGN * CLEF_HIP_KV_ALIGN;
+    }
     if ((int)ents.size() > max_blocks) return fail(err, errlen, "plan needs %zu blocks, room for %d", ents.size(), max_blocks);
     if (total_kv > max_kv) return fail(err, errlen, "plan needs %d kv rows, room for %d", total_kv, max_kv);
     if ((!blocks && !ents.empty()) || (!kv_tok && total_kv)) return fail(err, errlen, "missing plan output arrays");

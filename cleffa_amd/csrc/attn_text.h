@@ -115,7 +115,6 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     // ---- tiles
     const uint16_t *kbase = p.k_plane + ((size_t)kh * p.kvT + k_row0) * HD;
     const uint16_t *vbase = p.vt_plane + (size_t)kh * HD * p.kvT + k_row0;
-    const int last_chunk = ((k_len > 0 ? k_len - 1 : 0) / 8) * 8;
 
     // Wave w fills slots [(4w + j) * 64, +64) of each 2048-slot tile, one global_load_lds per j.
     // K slot s: key s/32, chunk (s%32) ^ k_swz(key). V^T slot s: dim s/8, chunk (s%8) ^ v_swz(dim).
@@ -125,25 +124,30 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     // V buffers from base + 64 KB, so the buffer choice is an immediate offset.
     uint16_t *const k0s = smem, *const k1s = smem + KTILE, *const v0s = smem + 2 * KTILE,
                    *const v1s = smem + 2 * KTILE + VTILE;
+    // Fills use a wave-uniform tile base plus loop-invariant per-lane byte offsets. Tiles may
+    // reach past the record's last key (up to the 64-key boundary): the plan sizes the planes so
+    // that those reads stay inside them, their scores are masked and their V^T entries zeroed.
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+    unsigned kfo[4], vfo[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int grp = wave_s * 4 + j;
+        const int key = grp * 2 + (lane >> 5);
+        kfo[j] = (unsigned)(key * HD + (((lane & 31) ^ k_swz(key)) * 8)) * 2u;
+        const int d = grp * 8 + (lane >> 3);
+        vfo[j] = ((unsigned)d * (unsigned)p.kvT + (unsigned)(((lane & 7) ^ v_swz(d)) * 8)) * 2u;
+    }
     auto load_tiles = [&](int kb, uint16_t *Ks, uint16_t *Vs) {
+        const char *kt_base = (const char *)(kbase + (size_t)kb * HD);
+        const char *vt_base = (const char *)(vbase + kb);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int grp = wave * 4 + j;
-            const int key = grp * 2 + (lane >> 5);
-            const int c = (lane & 31) ^ k_swz(key);
-            const int krow = min(kb + key, k_len - 1);
-            __builtin_amdgcn_global_load_lds((const void *)(kbase + (size_t)krow * HD + c * 8),
-                                             (lds_void *)(Ks + grp * 512), 16, 0, 0);
-        }
+        for (int j = 0; j < 4; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(kt_base + kfo[j]),
+                                             (lds_void *)(Ks + (wave_s * 4 + j) * 512), 16, 0, 0);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int grp = wave * 4 + j;
-            const int d = grp * 8 + (lane >> 3);
-            const int c = (lane & 7) ^ v_swz(d);
-            const int kk = min(kb + c * 8, last_chunk);
-            __builtin_amdgcn_global_load_lds((const void *)(vbase + (size_t)d * p.kvT + kk),
-                                             (lds_void *)(Vs + grp * 512), 16, 0, 0);
-        }
+        for (int j = 0; j < 4; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[j]),
+                                             (lds_void *)(Vs + (wave_s * 4 + j) * 512), 16, 0, 0);
     };
     // Gate rows of the block (128 x 256 bf16 = 64 KB): rows 0-63 into G0, 64-127 into G1, slot
     // s of a half = row s/32, 16-byte chunk (s%32) ^ (row & 15).
@@ -311,30 +315,31 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
         if (t + 1 < n_tiles) load_tiles(kb + BK, Kn, Vn);
         else if (p.gate) load_gate(Kn, Vn);   // the idle buffers take the epilogue's gate rows
         if (wave_live && (!p.causal || kb <= wave_last_pos)) {
-            // S^T: 32 MFMAs (4 key tiles x 8 dim chunks). K operands are read DEPTH steps ahead
-            // of their product so the LDS latency overlaps the matrix work.
+            // S^T: 32 MFMAs (4 key tiles x 8 dim chunks), chunk-major so consecutive products
+            // go to different accumulators. K operands are read DEPTH steps ahead of their
+            // product so the LDS latency overlaps the matrix work.
             constexpr int DEPTH = 6, QK = 4 * NC;
             f32x4 s[4];
             bf16x8 ring[DEPTH];
             static_for<DEPTH>([&](auto I) {
-                constexpr int st = decltype(I)::value, kt = st / NC, c = st % NC;
+                constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
                 ring[st] = lds_read16<buf * 2 * KTILE + (c >> 2) * 256>(ka[kt][c & 3]);
             });
             static_for<QK>([&](auto I) {
-                constexpr int st = decltype(I)::value, kt = st / NC, c = st % NC;
+                constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
                 constexpr int ahead = (QK - 1 - st) < (DEPTH - 1) ? (QK - 1 - st) : (DEPTH - 1);
                 bf16x8 a = ring[st % DEPTH];
                 lds_wait<ahead>(a);
                 if constexpr (c == 0) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
                 s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[kt], 0, 0, 0);
                 if constexpr (st + DEPTH < QK) {
-                    constexpr int n = st + DEPTH, nkt = n / NC, nc = n % NC;
+                    constexpr int n = st + DEPTH, nkt = n & 3, nc = n >> 2;
                     ring[st % DEPTH] = lds_read16<buf * 2 * KTILE + (nc >> 2) * 256>(ka[nkt][nc & 3]);
                 }
             });
             // first V operands, in flight during the softmax
-            auto vread = [&](auto I) {   // step st = 2 * mt + kc
-                constexpr int st = decltype(I)::value, mt = st >> 1, kc = st & 1;
+            auto vread = [&](auto I) {   // step st = 16 * kc + mt
+                constexpr int st = decltype(I)::value, mt = st & 15, kc = st >> 4;
                 constexpr int off = buf * 2 * VTILE + (32 * (mt >> 1) + 4 * (mt & 1)) * BK * 2;
                 return lds_read16<off>(kc ? va1 : va0);
             };
@@ -385,8 +390,8 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
 #pragma unroll
                 for (int mt = 0; mt < 16; mt++) o[mt] *= alpha;
             }
-            static_for<32>([&](auto I) {   // O^T: 32 MFMAs, same read-ahead
-                constexpr int st = decltype(I)::value, mt = st >> 1, kc = st & 1;
+            static_for<32>([&](auto I) {   // O^T: 32 MFMAs over 16 rotating accumulators, same read-ahead
+                constexpr int st = decltype(I)::value, mt = st & 15, kc = st >> 4;
                 constexpr int ahead = (31 - st) < (DEPTH - 1) ? (31 - st) : (DEPTH - 1);
                 bf16x8 a = vring[st % DEPTH];
                 lds_wait<ahead>(a);

@@ -68,7 +68,8 @@ int clef_hip_attn_plan_max_kv_rows(int n_seq, int Tk);
  * cached, and its queries are the last tokens. causal = 0 gives bidirectional attention within
  * each record (vision). Outputs: blocks [max_blocks][8] (sorted longest first), kv_tok [max_kv]
  * (pass row whose K/V lands in that kv row, or -1), *n_blk, *kv_rows (rows per head the K and
- * V^T planes need; a multiple of 64). */
+ * V^T planes need: every record's first kv row plus its key count rounded up to 64, since the
+ * attention kernel reads whole 64-key tiles). */
 bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int causal,
                         int32_t *blocks, int max_blocks, int32_t *kv_tok, int max_kv,
                         int *n_blk, int *kv_rows, char *err, size_t errlen);
