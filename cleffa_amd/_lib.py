@@ -17,7 +17,7 @@ BLOCK_INTS = 8
 # Every symbol include/clef_hip_attn.h declares.
 EXPORTS = (
     "clef_hip_attn_version", "clef_hip_attn_wave_size", "clef_hip_attn_init",
-    "clef_hip_attn_plan_max_blocks", "clef_hip_attn_plan_max_kv_rows", "clef_hip_attn_plan",
+    "clef_hip_attn_plan_max_blocks", "clef_hip_attn_plan",
     "clef_hip_rope_inv_freq", "clef_hip_vis_positions", "clef_hip_attn_prep_kv",
     "clef_hip_attn_core", "clef_hip_attn_prefill", "clef_hip_vis_attention",
 )
@@ -31,7 +31,7 @@ class AttnArgs(ctypes.Structure):
         ("qkv", c_void_p), ("q_norm", c_void_p), ("k_norm", c_void_p), ("pos3", c_void_p),
         ("inv_freq", c_void_p), ("rope_cs", c_void_p), ("k_plane", c_void_p), ("vt_plane", c_void_p),
         ("kvT", c_int), ("blocks", c_void_p), ("n_blk", c_int),
-        ("kv_tok", c_void_p),
+        ("tok_kv", c_void_p),
         ("kv_rows", c_int), ("causal", c_int), ("gate", c_int),
         ("out", c_void_p), ("out_type", c_int), ("f16_lim", c_float), ("ovf", c_void_p),
         ("trace", c_void_p),
@@ -43,7 +43,7 @@ class VisArgs(ctypes.Structure):
         ("P", c_int), ("heads", c_int), ("hd", c_int), ("scale", c_float),
         ("qkv", c_void_p), ("bias", c_void_p), ("pos2", c_void_p), ("inv_freq", c_void_p),
         ("q_plane", c_void_p), ("k_plane", c_void_p), ("vt_plane", c_void_p), ("kvT", c_int),
-        ("blocks", c_void_p), ("n_blk", c_int), ("kv_tok", c_void_p), ("kv_rows", c_int),
+        ("blocks", c_void_p), ("n_blk", c_int), ("tok_kv", c_void_p), ("kv_rows", c_int),
         ("out", c_void_p), ("out_type", c_int), ("f16_lim", c_float), ("ovf", c_void_p),
     ]
 
@@ -66,8 +66,6 @@ def load():
     lib.clef_hip_attn_init.restype = c_bool
     lib.clef_hip_attn_plan_max_blocks.argtypes = [c_int, c_int]
     lib.clef_hip_attn_plan_max_blocks.restype = c_int
-    lib.clef_hip_attn_plan_max_kv_rows.argtypes = [c_int, c_int]
-    lib.clef_hip_attn_plan_max_kv_rows.restype = c_int
     lib.clef_hip_attn_plan.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int, c_int,
                                        POINTER(c_int32), c_int, POINTER(c_int32), c_int,
                                        POINTER(c_int), POINTER(c_int), c_char_p, c_size_t]

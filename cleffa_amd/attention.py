@@ -107,25 +107,23 @@ class AttnPlan:
         if self.cu_k is not None and len(self.cu_k) != len(cu_q):
             raise ValueError("cu_seqlens_k must have as many entries as cu_seqlens_q")
         self.causal = bool(causal)
-        tk = self.T if self.cu_k is None else int(self.cu_k[-1])
         max_blk = lib.clef_hip_attn_plan_max_blocks(self.n_seq, self.T)
-        max_kv = lib.clef_hip_attn_plan_max_kv_rows(self.n_seq, tk)
         blocks = np.zeros((max(max_blk, 1), BLOCK_INTS), dtype=np.int32)
-        kv_tok = np.zeros(max(max_kv, 1), dtype=np.int32)
+        tok_kv = np.zeros(max(self.T, 1), dtype=np.int32)
         n_blk, kv_rows = ctypes.c_int(0), ctypes.c_int(0)
         err = _err()
         ok = lib.clef_hip_attn_plan(_i32p(cu_q), None if self.cu_k is None else _i32p(self.cu_k),
                                     self.n_seq, int(self.causal), _i32p(blocks), max_blk,
-                                    _i32p(kv_tok), max_kv, ctypes.byref(n_blk), ctypes.byref(kv_rows),
+                                    _i32p(tok_kv), self.T, ctypes.byref(n_blk), ctypes.byref(kv_rows),
                                     err, len(err))
         _lib.check(ok, err)
         self.n_blk = n_blk.value
         self.kv_rows = kv_rows.value
         self.blocks_host = blocks[: self.n_blk].copy()
-        self.kv_tok_host = kv_tok[: self.kv_rows].copy()
+        self.tok_kv_host = tok_kv[: self.T].copy()
         self.device = _device(device)
         self.blocks = torch.from_numpy(np.ascontiguousarray(blocks[: max(self.n_blk, 1)])).to(self.device)
-        self.kv_tok = torch.from_numpy(np.ascontiguousarray(kv_tok[: max(self.kv_rows, 1)])).to(self.device)
+        self.tok_kv = torch.from_numpy(np.ascontiguousarray(tok_kv)).to(self.device)
         # kv rows the planes must hold, rounded to the 16-byte V^T chunk
         self.kvT = max(8, (self.kv_rows + 7) // 8 * 8)
 
@@ -215,7 +213,7 @@ class TextAttention:
         a.pos3, a.inv_freq, a.rope_cs = _ptr(pos3), _ptr(self.inv_freq), _ptr(rope_cs)
         a.k_plane, a.vt_plane, a.kvT = _ptr(k_plane), _ptr(vt_plane), kvT
         a.blocks, a.n_blk = _ptr(plan.blocks), plan.n_blk
-        a.kv_tok, a.kv_rows = _ptr(plan.kv_tok), plan.kv_rows
+        a.tok_kv, a.kv_rows = _ptr(plan.tok_kv), plan.kv_rows
         a.causal, a.gate = int(plan.causal), int(gate)
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
         a.trace = _ptr(trace)
@@ -288,7 +286,7 @@ class VisionAttention:
         a.P, a.heads, a.hd, a.scale = P, self.heads, self.hd, self.scale
         a.qkv, a.bias, a.pos2, a.inv_freq = _ptr(qkv), _ptr(bias), _ptr(pos2), _ptr(self.inv_freq)
         a.q_plane, a.k_plane, a.vt_plane, a.kvT = _ptr(q_plane), _ptr(k_plane), _ptr(vt_plane), kvT
-        a.blocks, a.n_blk, a.kv_tok, a.kv_rows = _ptr(plan.blocks), plan.n_blk, _ptr(plan.kv_tok), plan.kv_rows
+        a.blocks, a.n_blk, a.tok_kv, a.kv_rows = _ptr(plan.blocks), plan.n_blk, _ptr(plan.tok_kv), plan.kv_rows
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
         err = _err()
         _lib.check(lib.clef_hip_vis_attention(ctypes.byref(a), _stream_handle(stream), err, len(err)), err)

@@ -69,8 +69,8 @@ bool check_text(const clef_hip_attn_args *a, bool need_core, char *err, size_t e
         if (!a->out || !aligned16(a->out)) return fail(err, errlen, "out must be a 16-byte aligned device pointer");
         if (a->out_type < CLEF_HIP_OUT_BF16 || a->out_type > CLEF_HIP_OUT_F32) return fail(err, errlen, "bad out_type %d", a->out_type);
         if (!(a->scale > 0.f)) return fail(err, errlen, "bad scale");
-    } else if (a->kv_rows && !a->kv_tok) {
-        return fail(err, errlen, "missing kv_tok");
+    } else if (a->T && !a->tok_kv) {
+        return fail(err, errlen, "missing tok_kv");
     }
     return true;
 }
@@ -101,13 +101,9 @@ int clef_hip_attn_plan_max_blocks(int n_seq, int Tq) {
     return Tq / CLEF_HIP_BLOCK_Q + n_seq + 1;
 }
 
-int clef_hip_attn_plan_max_kv_rows(int n_seq, int Tk) {
-    if (n_seq < 0 || Tk < 0) return 0;
-    return Tk + CLEF_HIP_KV_ALIGN * (n_seq + 1);
-}
 
 bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int causal,
-                        int32_t *blocks, int max_blocks, int32_t *kv_tok, int max_kv,
+                        int32_t *blocks, int max_blocks, int32_t *tok_kv, int max_tok,
                         int *n_blk, int *kv_rows, char *err, size_t errlen) {
     if (!cu_q || n_seq < 0 || !n_blk || !kv_rows) return fail(err, errlen, "bad plan arguments");
     if (cu_q[0] != 0) return fail(err, errlen, "cu_seqlens_q must start at 0");
@@ -153,19 +149,18 @@ bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int
         if (!cu_k) kv_off += (nq + CLEF_HIP_KV_ALIGN - 1) / CLEF_HIP_KV_ALIGN * CLEF_HIP_KV_ALIGN;
     }
     if ((int)ents.size() > max_blocks) return fail(err, errlen, "plan needs %zu blocks, room for %d", ents.size(), max_blocks);
-    if (total_kv > max_kv) return fail(err, errlen, "plan needs %d kv rows, room for %d", total_kv, max_kv);
-    if ((!blocks && !ents.empty()) || (!kv_tok && total_kv)) return fail(err, errlen, "missing plan output arrays");
+    if (cu_q[n_seq] > max_tok) return fail(err, errlen, "plan needs %d tok_kv entries, room for %d", cu_q[n_seq], max_tok);
+    if ((!blocks && !ents.empty()) || (!tok_kv && cu_q[n_seq])) return fail(err, errlen, "missing plan output arrays");
     // Longest key range first, so the long causal blocks start early (clef_metal.m:1243-1257
     // orders each record's blocks longest first; here the order is global across records).
     std::stable_sort(ents.begin(), ents.end(), [](const Ent &x, const Ent &y) { return x.v[4] > y.v[4]; });
     for (size_t i = 0; i < ents.size(); i++) memcpy(blocks + CLEF_HIP_BLOCK_INTS * i, ents[i].v, sizeof(ents[i].v));
-    for (int i = 0; i < total_kv; i++) kv_tok[i] = -1;
     kv_off = 0;
     for (int r = 0; r < n_seq; r++) {
         const int nq = cu_q[r + 1] - cu_q[r];
         const int nk = cu_k ? cu_k[r + 1] - cu_k[r] : nq;
         const int k0 = cu_k ? cu_k[r] : kv_off;
-        for (int j = 0; j < nq; j++) kv_tok[k0 + (nk - nq) + j] = cu_q[r] + j;
+        for (int j = 0; j < nq; j++) tok_kv[cu_q[r] + j] = k0 + (nk - nq) + j;
         if (!cu_k) kv_off += (nq + CLEF_HIP_KV_ALIGN - 1) / CLEF_HIP_KV_ALIGN * CLEF_HIP_KV_ALIGN;
     }
     *n_blk = (int)ents.size();
@@ -195,13 +190,13 @@ bool clef_hip_vis_positions(const int32_t *cu, int n_img, const int32_t *grid_w,
 
 bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {
     if (!check_text(a, false, err, errlen)) return false;
-    if (a->kv_rows == 0) return true;
+    if (a->T == 0) return true;
     PrepParams p;
     p.qkv = a->qkv; p.k_norm = a->k_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
-    p.kv_tok = a->kv_tok; p.k_plane = a->k_plane; p.vt_plane = a->vt_plane;
-    p.row = a->row; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
-    p.kv_rows = a->kv_rows; p.eps = a->eps; p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
-    dim3 grid((a->kv_rows + 15) / 16, a->nkv);
+    p.tok_kv = a->tok_kv; p.k_plane = a->k_plane; p.vt_plane = a->vt_plane;
+    p.T = a->T; p.row = a->row; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
+    p.eps = a->eps; p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
+    dim3 grid((a->T + 15) / 16, a->nkv);
     hipLaunchKernelGGL(text_prep_kv_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
     return launch_ok("text_prep_kv", err, errlen);
 }
@@ -246,13 +241,13 @@ bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err,
     if (!aligned16(a->q_plane) || !aligned16(a->k_plane) || !aligned16(a->vt_plane) || !aligned16(a->out))
         return fail(err, errlen, "vision planes and output must be 16-byte aligned");
     if (a->out_type < CLEF_HIP_OUT_BF16 || a->out_type > CLEF_HIP_OUT_F32) return fail(err, errlen, "bad out_type %d", a->out_type);
-    if ((a->n_blk && !a->blocks) || (a->kv_rows && !a->kv_tok)) return fail(err, errlen, "missing plan");
-    if (a->kv_rows) {
+    if ((a->n_blk && !a->blocks) || (a->P && !a->tok_kv)) return fail(err, errlen, "missing plan");
+    if (a->P) {
         VisPrepParams q;
-        q.qkv = a->qkv; q.bias = a->bias; q.pos2 = a->pos2; q.inv_freq = a->inv_freq; q.kv_tok = a->kv_tok;
+        q.qkv = a->qkv; q.bias = a->bias; q.pos2 = a->pos2; q.inv_freq = a->inv_freq; q.tok_kv = a->tok_kv;
         q.q_plane = a->q_plane; q.k_plane = a->k_plane; q.vt_plane = a->vt_plane;
-        q.P = a->P; q.heads = a->heads; q.kvT = a->kvT; q.kv_rows = a->kv_rows;
-        hipLaunchKernelGGL(vis_prep_kernel, dim3((a->kv_rows + 63) / 64, a->heads), dim3(256), 0, (hipStream_t)stream, q);
+        q.P = a->P; q.heads = a->heads; q.kvT = a->kvT;
+        hipLaunchKernelGGL(vis_prep_kernel, dim3((a->P + 15) / 16, a->heads), dim3(256), 0, (hipStream_t)stream, q);
         if (!launch_ok("vis_prep", err, errlen)) return false;
     }
     if (a->n_blk == 0) return true;

@@ -518,15 +518,15 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
     }
 }
 // ------------------------------------------------------------------------------------------
-// Text K/V prologue (metal/clef.metal:245-300 and 873-928 for K and V): per kv row of the
-// plan, K = RMSNorm(k) * (1+w) then partial rotary, written to the K plane [nkv][kvT][HD];
-// V copied unnormalised and written transposed to the V^T plane [nkv][HD][kvT]. Rows whose
-// kv_tok is negative (cached prefix rows, alignment padding) are left untouched. When rope_cs
-// is set, the cos/sin of every pass row's rotary angles are also written there ([T][n_rot/2]
-// float2) for the attention kernel's Q prologue.
-// Grid (kv_rows / 16, nkv), 256 threads. A row is handled by 32 lanes with 8 dims each
-// (16-byte loads and stores); the RMS sum reduces over DPP rows, a rotary pair (i, i + 32)
-// sits in lanes 4 apart.
+// Text K/V prologue (metal/clef.metal:245-300 and 873-928 for K and V): for every pass row t,
+// K = RMSNorm(k) * (1+w) then partial rotary, written to row tok_kv[t] of the K plane
+// [nkv][kvT][HD]; V copied unnormalised and written transposed into the V^T plane
+// [nkv][HD][kvT]. Rows of the planes that no pass row maps to (cached prefix rows, alignment
+// padding) are left untouched. When rope_cs is set, the cos/sin of every pass row's rotary
+// angles are also written there ([T][n_rot/2] float2) for the attention kernel's Q prologue.
+// Grid (T / 16, nkv), 256 threads. The workgroup's rows are consecutive pass rows, so the
+// qkv loads need no lookup. A row is handled by 32 lanes with 8 dims each; the RMS sum
+// reduces over DPP rows, a rotary pair (i, i + 32) sits in lanes 4 apart.
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ float row16_sum(float v) {   // sum over the lane's 16-lane row
     v += __builtin_amdgcn_update_dpp(0.f, v, 0x128, 0xf, 0xf, false);   // row_ror:8
@@ -537,33 +537,46 @@ __device__ __forceinline__ float row16_sum(float v) {   // sum over the lane's 1
 }
 
 __global__ __launch_bounds__(256) void text_prep_kv_kernel(PrepParams p) {
-    constexpr int HD = 256, ROWS = 16;           // kv rows per workgroup
+    constexpr int HD = 256, ROWS = 16;           // pass rows per workgroup
     constexpr int VS = HD + 8;                   // LDS row stride of the V tile
     __shared__ __attribute__((aligned(16))) uint16_t vr[ROWS * VS];
-    __shared__ int toks[ROWS];
+    __shared__ int krows[ROWS];
     const int tid = threadIdx.x;
     const int c = tid & 31, rl = tid >> 5;       // 8-dim chunk of the row, row within a pass
-    const int row0 = blockIdx.x * ROWS, kh = blockIdx.y;
-    if (tid < ROWS) toks[tid] = (row0 + tid < p.kv_rows) ? p.kv_tok[row0 + tid] : -1;
-    __syncthreads();
+    const int t0 = blockIdx.x * ROWS, kh = blockIdx.y;
+    const int half_rot = p.n_rot / 2;   // 0 or 32: chunks 0-3 pair with chunks 4-7
+    // every global load is issued before the first use
     u32x4 kw[2], vw[2];
+    int pos[2][8];
 #pragma unroll
     for (int it = 0; it < 2; it++) {
-        const int tok = toks[it * 8 + rl];
-        const uint16_t *src = p.qkv + (size_t)(tok < 0 ? 0 : tok) * p.row + (size_t)p.nh * 2 * HD + (size_t)kh * HD + c * 8;
-        kw[it] = tok >= 0 ? *(const u32x4 *)src : u32x4{0, 0, 0, 0};
-        vw[it] = tok >= 0 ? *(const u32x4 *)(src + (size_t)p.nkv * HD) : u32x4{0, 0, 0, 0};
+        const int t = t0 + it * 8 + rl;
+        const bool ok = t < p.T;
+        const uint16_t *src = p.qkv + (size_t)(ok ? t : 0) * p.row + (size_t)p.nh * 2 * HD + (size_t)kh * HD + c * 8;
+        kw[it] = ok ? *(const u32x4 *)src : u32x4{0, 0, 0, 0};
+        vw[it] = ok ? *(const u32x4 *)(src + (size_t)p.nkv * HD) : u32x4{0, 0, 0, 0};
+        if (half_rot && c < 8) {
+            const int32_t *pp = p.pos3 + 3 * (size_t)(ok ? t : 0);
+#pragma unroll
+            for (int e = 0; e < 8; e++) pos[it][e] = pp[((c & 3) * 8 + e) % 3];
+        }
     }
-    float wn[8];
+    if (tid < ROWS) krows[tid] = t0 + tid < p.T ? p.tok_kv[t0 + tid] : -1;
+    float wn[8], fr[8];
     if (p.k_norm) {
         const float4 w0 = *(const float4 *)(p.k_norm + c * 8), w1 = *(const float4 *)(p.k_norm + c * 8 + 4);
         wn[0] = w0.x; wn[1] = w0.y; wn[2] = w0.z; wn[3] = w0.w; wn[4] = w1.x; wn[5] = w1.y; wn[6] = w1.z; wn[7] = w1.w;
     }
-    const int half_rot = p.n_rot / 2;   // 0 or 32: chunks 0-3 pair with chunks 4-7
+    if (half_rot && c < 8) {
+        const float4 f0 = *(const float4 *)(p.inv_freq + (c & 3) * 8), f1 = *(const float4 *)(p.inv_freq + (c & 3) * 8 + 4);
+        fr[0] = f0.x; fr[1] = f0.y; fr[2] = f0.z; fr[3] = f0.w; fr[4] = f1.x; fr[5] = f1.y; fr[6] = f1.z; fr[7] = f1.w;
+    }
+    __syncthreads();
 #pragma unroll
     for (int it = 0; it < 2; it++) {
         const int rr = it * 8 + rl;
-        const int tok = toks[rr];
+        const int t = t0 + rr;
+        const int krow = krows[rr];
         float x[8];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -590,75 +603,64 @@ __global__ __launch_bounds__(256) void text_prep_kv_kernel(PrepParams p) {
                 const float dn = __builtin_amdgcn_update_dpp(0.f, x[e], 0x124, 0xf, 0xf, false);   // lane - 4
                 y[e] = (c & 4) ? dn : up;
             }
-            if (c < 8 && tok >= 0) {
+            if (c < 8 && t < p.T) {
                 const bool first = c < 4;
-                const int32_t *pp = p.pos3 + 3 * (size_t)tok;
-                float *cs = p.rope_cs ? p.rope_cs + (size_t)tok * 2 * half_rot : nullptr;
+                float *cs = p.rope_cs ? p.rope_cs + (size_t)t * 2 * half_rot : nullptr;
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const int i = (c & 3) * 8 + e;
                     float sn, cn;
-                    sincosf((float)pp[i % 3] * p.inv_freq[i], &sn, &cn);
+                    sincosf((float)pos[it][e] * fr[e], &sn, &cn);
                     x[e] = first ? x[e] * cn - y[e] * sn : x[e] * cn + y[e] * sn;
                     if (cs && first) *(float2 *)(cs + 2 * i) = make_float2(cn, sn);
                 }
             }
         }
-        if (tok >= 0) {
+        if (krow >= 0) {
             u32x4 ko = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7])};
-            *(u32x4 *)(p.k_plane + ((size_t)kh * p.kvT + row0 + rr) * HD + c * 8) = ko;
+            *(u32x4 *)(p.k_plane + ((size_t)kh * p.kvT + krow) * HD + c * 8) = ko;
         }
         *(u32x4 *)(vr + rr * VS + c * 8) = vw[it];
     }
     __syncthreads();
-    // V^T: HD dims x 16 keys, two 8-key chunks per dim
+    // V^T: lane e of each 16-lane group writes row e's value of one dim (2 bytes); a group's
+    // 16 stores cover consecutive kv rows of one V^T row.
+    const int e = tid & 15;
+    const int krow = krows[e];
 #pragma unroll
-    for (int q = 0; q < 2; q++) {
-        const int id = tid + 256 * q;
-        const int d = id >> 1, c8 = id & 1;
-        uint16_t v[8];
-        bool all = true;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            v[e] = vr[(c8 * 8 + e) * VS + d];
-            all = all && toks[c8 * 8 + e] >= 0;
-        }
-        uint16_t *dst = p.vt_plane + ((size_t)kh * HD + d) * p.kvT + row0 + c8 * 8;
-        if (all) {
-            u32x4 w = {(unsigned)v[0] | ((unsigned)v[1] << 16), (unsigned)v[2] | ((unsigned)v[3] << 16),
-                       (unsigned)v[4] | ((unsigned)v[5] << 16), (unsigned)v[6] | ((unsigned)v[7] << 16)};
-            *(u32x4 *)dst = w;
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                if (toks[c8 * 8 + e] >= 0) dst[e] = v[e];
-        }
+    for (int q = 0; q < HD / 16; q++) {
+        const int d = q * 16 + (tid >> 4);
+        if (krow >= 0) p.vt_plane[((size_t)kh * HD + d) * p.kvT + krow] = vr[e * VS + d];
     }
 }
 
 // ------------------------------------------------------------------------------------------
 // Vision prologue (metal/clef.metal:1616-1656, vis_qkv_rope): qkv [P][3E] (+ bias) ->
-// Q plane [heads][P][VHDK], K plane [heads][kvT][VHDK] (rows kv_row), V^T [heads][VHD][kvT].
-// Q and K take the 2-D rotary: pair (i, i + hd/2); the first hd/4 pairs turn by the patch's
-// grid row, the rest by its column. pos2 [P][2] holds each patch's (row, column).
-// Grid (kv_rows / 64, heads), 256 threads; lane i < hd/2 of a wave owns dims i and i + hd/2.
+// Q plane [heads][P][VHDK] (row = patch), K plane [heads][kvT][VHDK] (row tok_kv[patch]),
+// V^T [heads][VHD][kvT]. Q and K take the 2-D rotary: pair (i, i + hd/2); the first hd/4
+// pairs turn by the patch's grid row, the rest by its column; pos2 [P][2] holds each patch's
+// (row, column). Grid (P / 16, heads), 256 threads: 16 lanes per patch, lane j owns the rotary
+// pairs j, j + 16 and (j < 4) j + 32.
 // ------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void vis_prep_kernel(VisPrepParams p) {
-    constexpr int HD = 72, HDK = 80, ROWS = 64, HALF = HD / 2, QUART = HD / 4;
-    __shared__ __attribute__((aligned(16))) uint16_t vt[HD * (ROWS + 8)];
-    __shared__ int toks[ROWS];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int row0 = blockIdx.x * ROWS, h = blockIdx.y;
+    constexpr int HD = 72, HDK = 80, ROWS = 16, HALF = HD / 2, QUART = HD / 4, VS = HD + 8;
+    __shared__ __attribute__((aligned(16))) uint16_t vr[ROWS * VS];
+    __shared__ int krows[ROWS];
+    const int tid = threadIdx.x, rr = tid >> 4, j = tid & 15;
+    const int t0 = blockIdx.x * ROWS, h = blockIdx.y;
     const int E = p.heads * HD;
-    if (tid < ROWS) toks[tid] = (row0 + tid < p.kv_rows) ? p.kv_tok[row0 + tid] : -1;
+    const int tok = t0 + rr;
+    if (tid < ROWS) krows[tid] = t0 + tid < p.P ? p.tok_kv[t0 + tid] : -1;
     __syncthreads();
-    for (int r = wave * 16; r < wave * 16 + 16; r++) {
-        const int tok = toks[r];
-        if (tok < 0) continue;
-        const int kvr = row0 + r;
+    const int krow = krows[rr];
+    if (tok < p.P) {
         const uint16_t *row = p.qkv + (size_t)tok * 3 * E;
-        if (lane < HALF) {
-            const int i = lane;
+        uint16_t *qd = p.q_plane + ((size_t)h * p.P + tok) * HDK;
+        uint16_t *kd = krow >= 0 ? p.k_plane + ((size_t)h * p.kvT + krow) * HDK : nullptr;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const int i = j + 16 * k;
+            if (i >= HALF) break;
             const float ang = (float)p.pos2[2 * tok + (i < QUART ? 0 : 1)] * p.inv_freq[i < QUART ? i : i - QUART];
             float sn, cs;
             sincosf(ang, &sn, &cs);
@@ -668,38 +670,27 @@ __global__ __launch_bounds__(256) void vis_prep_kernel(VisPrepParams p) {
                 float x0 = bf2f(row[base + i]), x1 = bf2f(row[base + i + HALF]);
                 if (p.bias) { x0 += p.bias[base + i]; x1 += p.bias[base + i + HALF]; }
                 const float y0 = x0 * cs - x1 * sn, y1 = x1 * cs + x0 * sn;
-                uint16_t *dst = part == 0 ? p.q_plane + ((size_t)h * p.P + tok) * HDK
-                                          : p.k_plane + ((size_t)h * p.kvT + kvr) * HDK;
-                dst[i] = f2bf(y0);
-                dst[i + HALF] = f2bf(y1);
+                uint16_t *dst = part == 0 ? qd : kd;
+                if (dst) {
+                    dst[i] = f2bf(y0);
+                    dst[i + HALF] = f2bf(y1);
+                }
             }
             const int vb = 2 * E + h * HD;
             float v0 = bf2f(row[vb + i]), v1 = bf2f(row[vb + i + HALF]);
             if (p.bias) { v0 += p.bias[vb + i]; v1 += p.bias[vb + i + HALF]; }
-            vt[i * (ROWS + 8) + r] = f2bf(v0);
-            vt[(i + HALF) * (ROWS + 8) + r] = f2bf(v1);
-        } else if (lane < HALF + (HDK - HD)) {
-            // zero the contraction padding dims of Q and K
-            const int d = HD + (lane - HALF);
-            p.q_plane[((size_t)h * p.P + tok) * HDK + d] = 0;
-            p.k_plane[((size_t)h * p.kvT + kvr) * HDK + d] = 0;
+            vr[rr * VS + i] = f2bf(v0);
+            vr[rr * VS + i + HALF] = f2bf(v1);
+        }
+        if (j < HDK - HD) {   // zero the contraction padding dims of Q and K
+            qd[HD + j] = 0;
+            if (kd) kd[HD + j] = 0;
         }
     }
     __syncthreads();
-    for (int id = tid; id < HD * (ROWS / 8); id += 256) {
-        const int d = id / (ROWS / 8), c8 = id % (ROWS / 8);
-        uint16_t *dst = p.vt_plane + ((size_t)h * HD + d) * p.kvT + row0 + c8 * 8;
-        bool all = true;
-#pragma unroll
-        for (int e = 0; e < 8; e++) all = all && toks[c8 * 8 + e] >= 0;
-        if (all) {
-            *(u32x4 *)dst = *(const u32x4 *)(vt + d * (ROWS + 8) + c8 * 8);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                if (toks[c8 * 8 + e] >= 0) dst[e] = vt[d * (ROWS + 8) + c8 * 8 + e];
-        }
-    }
+    const int e = tid & 15, ke = krows[e];
+    for (int d = tid >> 4; d < HD; d += 16)
+        if (ke >= 0) p.vt_plane[((size_t)h * HD + d) * p.kvT + ke] = vr[e * VS + d];
 }
 
 }  // namespace clef_hip

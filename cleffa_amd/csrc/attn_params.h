@@ -30,11 +30,11 @@ struct PrepParams {
     const float *k_norm;
     const int32_t *pos3;
     const float *inv_freq;
-    const int32_t *kv_tok;
+    const int32_t *tok_kv;    // kv row of each pass row
     uint16_t *k_plane;
     uint16_t *vt_plane;
     float *rope_cs;
-    int row, nh, nkv, n_rot, kvT, kv_rows;
+    int T, row, nh, nkv, n_rot, kvT;
     float eps;
 };
 
@@ -43,11 +43,11 @@ struct VisPrepParams {
     const float *bias;
     const int32_t *pos2;
     const float *inv_freq;
-    const int32_t *kv_tok;
+    const int32_t *tok_kv;
     uint16_t *q_plane;
     uint16_t *k_plane;
     uint16_t *vt_plane;
-    int P, heads, kvT, kv_rows;
+    int P, heads, kvT;
 };
 
 }  // namespace clef_hip
