@@ -1,0 +1,82 @@
+"""Host-side plan builder (clef_hip_attn_plan, the block list of clef_metal.m:1243-1257 and the
+packing of clef.c:470-497): coverage, key ranges, order and kv-row layout. Runs on the CPU."""
+import numpy as np
+import pytest
+
+from cleffa_amd import AttnPlan
+from cleffa_amd._lib import BLOCK_Q, KV_ALIGN
+
+
+def _check_plan(cu_q, cu_k, causal):
+    plan = AttnPlan(cu_q, cu_k, causal=causal, device="cpu")
+    b = plan.blocks_host
+    T = int(cu_q[-1])
+    seen = np.zeros(T, np.int32)
+    for e in b:
+        q_row0, nq, q_pos0, k_row0, k_len, flag_row, rec, _ = (int(x) for x in e)
+        assert 1 <= nq <= BLOCK_Q
+        seen[q_row0:q_row0 + nq] += 1
+        lq = cu_q[rec + 1] - cu_q[rec]
+        lk = lq if cu_k is None else cu_k[rec + 1] - cu_k[rec]
+        L = lk - lq
+        i0 = q_row0 - cu_q[rec]
+        assert i0 % BLOCK_Q == 0 and q_pos0 == L + i0 and flag_row == cu_q[rec]
+        assert k_len == (min(lk, L + i0 + nq) if causal else lk)
+        if cu_k is not None:
+            assert k_row0 == cu_k[rec]
+        # whole 64-key tiles from the record's first key stay inside the planes
+        assert k_row0 + -(-lk // KV_ALIGN) * KV_ALIGN <= plan.kv_rows
+    assert (seen == 1).all(), "every pass row in exactly one block"
+    assert (np.diff(b[:, 4]) <= 0).all(), "blocks ordered longest first"
+    # pass row -> kv row: a record's tokens are its last keys, in order
+    for r in range(len(cu_q) - 1):
+        rows = plan.tok_kv_host[cu_q[r]:cu_q[r + 1]]
+        lq = cu_q[r + 1] - cu_q[r]
+        lk = lq if cu_k is None else cu_k[r + 1] - cu_k[r]
+        k0 = rows[0] - (lk - lq) if lq else None
+        if lq:
+            assert (np.diff(rows) == 1).all()
+            if cu_k is None:
+                assert k0 % KV_ALIGN == 0
+            else:
+                assert k0 == cu_k[r]
+    return plan
+
+
+@pytest.mark.parametrize("lengths", [[1], [1160, 890, 730, 425, 472, 136, 179, 104], [127, 128, 129, 1, 256],
+                                     [0, 5, 0, 300], [16384]])
+@pytest.mark.parametrize("causal", [True, False])
+def test_fresh_plans(lengths, causal):
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    plan = _check_plan(cu, None, causal)
+    assert plan.n_blk == sum(-(-n // BLOCK_Q) for n in lengths)
+
+
+def test_prefix_plan():
+    cu_q = np.array([0, 512, 1024, 1536, 2048], np.int32)
+    cu_k = np.array([0, 2560, 5120, 7680, 10240], np.int32)
+    plan = _check_plan(cu_q, cu_k, True)
+    assert plan.kv_rows == 10240
+    assert plan.pairs() == 4 * (512 * 2048 + 512 * 513 // 2)
+
+
+def test_empty_pass():
+    plan = AttnPlan(np.array([0], np.int32), device="cpu")
+    assert plan.n_blk == 0 and plan.kv_rows == 0
+
+
+@pytest.mark.parametrize("cu_q,cu_k,msg", [
+    ([0, 5, 3], None, "decreases"),
+    ([1, 5], None, "start at 0"),
+    ([0, 10], [0, 5], "keys for"),
+    ([0, 4, 8], [0, 12, 20], "not a multiple of 8"),
+])
+def test_plan_errors(cu_q, cu_k, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        AttnPlan(np.array(cu_q, np.int32), None if cu_k is None else np.array(cu_k, np.int32), device="cpu")
+
+
+def test_pairs_counts_causal_and_bidirectional():
+    cu = np.array([0, 3, 10], np.int32)
+    assert AttnPlan(cu, device="cpu").pairs() == 6 + 28
+    assert AttnPlan(cu, causal=False, device="cpu").pairs() == 9 + 49
