@@ -31,7 +31,7 @@ class AttnArgs(ctypes.Structure):
         ("qkv", c_void_p), ("q_norm", c_void_p), ("k_norm", c_void_p), ("pos3", c_void_p),
         ("inv_freq", c_void_p), ("rope_cs", c_void_p), ("k_plane", c_void_p), ("vt_plane", c_void_p),
         ("kvT", c_int), ("blocks", c_void_p), ("n_blk", c_int),
-        ("tok_kv", c_void_p),
+        ("kv_tok", c_void_p),
         ("kv_rows", c_int), ("causal", c_int), ("gate", c_int),
         ("out", c_void_p), ("out_type", c_int), ("f16_lim", c_float), ("ovf", c_void_p),
         ("trace", c_void_p),
@@ -68,6 +68,7 @@ def load():
     lib.clef_hip_attn_plan_max_blocks.restype = c_int
     lib.clef_hip_attn_plan.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int, c_int,
                                        POINTER(c_int32), c_int, POINTER(c_int32), c_int,
+                                       POINTER(c_int32), c_int,
                                        POINTER(c_int), POINTER(c_int), c_char_p, c_size_t]
     lib.clef_hip_attn_plan.restype = c_bool
     lib.clef_hip_rope_inv_freq.argtypes = [c_float, c_int, POINTER(c_float)]

@@ -110,20 +110,25 @@ class AttnPlan:
         max_blk = lib.clef_hip_attn_plan_max_blocks(self.n_seq, self.T)
         blocks = np.zeros((max(max_blk, 1), BLOCK_INTS), dtype=np.int32)
         tok_kv = np.zeros(max(self.T, 1), dtype=np.int32)
+        # plane rows: a fresh pass pads each record to 64 rows; a prefix pass ends at cu_k[-1] + 64
+        max_kv = (self.T + 64 * self.n_seq if self.cu_k is None else int(self.cu_k[-1]) + 64) + 64
+        kv_tok = np.zeros(max_kv, dtype=np.int32)
         n_blk, kv_rows = ctypes.c_int(0), ctypes.c_int(0)
         err = _err()
         ok = lib.clef_hip_attn_plan(_i32p(cu_q), None if self.cu_k is None else _i32p(self.cu_k),
                                     self.n_seq, int(self.causal), _i32p(blocks), max_blk,
-                                    _i32p(tok_kv), self.T, ctypes.byref(n_blk), ctypes.byref(kv_rows),
-                                    err, len(err))
+                                    _i32p(tok_kv), self.T, _i32p(kv_tok), max_kv,
+                                    ctypes.byref(n_blk), ctypes.byref(kv_rows), err, len(err))
         _lib.check(ok, err)
         self.n_blk = n_blk.value
         self.kv_rows = kv_rows.value
         self.blocks_host = blocks[: self.n_blk].copy()
         self.tok_kv_host = tok_kv[: self.T].copy()
+        self.kv_tok_host = kv_tok[: self.kv_rows].copy()
         self.device = _device(device)
         self.blocks = torch.from_numpy(np.ascontiguousarray(blocks[: max(self.n_blk, 1)])).to(self.device)
         self.tok_kv = torch.from_numpy(np.ascontiguousarray(tok_kv)).to(self.device)
+        self.kv_tok = torch.from_numpy(np.ascontiguousarray(kv_tok[: max(self.kv_rows, 1)])).to(self.device)
         # kv rows the planes must hold, rounded to the 16-byte V^T chunk
         self.kvT = max(8, (self.kv_rows + 7) // 8 * 8)
 
@@ -213,7 +218,7 @@ class TextAttention:
         a.pos3, a.inv_freq, a.rope_cs = _ptr(pos3), _ptr(self.inv_freq), _ptr(rope_cs)
         a.k_plane, a.vt_plane, a.kvT = _ptr(k_plane), _ptr(vt_plane), kvT
         a.blocks, a.n_blk = _ptr(plan.blocks), plan.n_blk
-        a.tok_kv, a.kv_rows = _ptr(plan.tok_kv), plan.kv_rows
+        a.kv_tok, a.kv_rows = _ptr(plan.kv_tok), plan.kv_rows
         a.causal, a.gate = int(plan.causal), int(gate)
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
         a.trace = _ptr(trace)

@@ -69,8 +69,8 @@ bool check_text(const clef_hip_attn_args *a, bool need_core, char *err, size_t e
         if (!a->out || !aligned16(a->out)) return fail(err, errlen, "out must be a 16-byte aligned device pointer");
         if (a->out_type < CLEF_HIP_OUT_BF16 || a->out_type > CLEF_HIP_OUT_F32) return fail(err, errlen, "bad out_type %d", a->out_type);
         if (!(a->scale > 0.f)) return fail(err, errlen, "bad scale");
-    } else if (a->T && !a->tok_kv) {
-        return fail(err, errlen, "missing tok_kv");
+    } else if (a->kv_rows && !a->kv_tok) {
+        return fail(err, errlen, "missing kv_tok");
     }
     return true;
 }
@@ -104,7 +104,7 @@ int clef_hip_attn_plan_max_blocks(int n_seq, int Tq) {
 
 bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int causal,
                         int32_t *blocks, int max_blocks, int32_t *tok_kv, int max_tok,
-                        int *n_blk, int *kv_rows, char *err, size_t errlen) {
+                        int32_t *kv_tok, int max_kv, int *n_blk, int *kv_rows, char *err, size_t errlen) {
     if (!cu_q || n_seq < 0 || !n_blk || !kv_rows) return fail(err, errlen, "bad plan arguments");
     if (cu_q[0] != 0) return fail(err, errlen, "cu_seqlens_q must start at 0");
     if (cu_k && cu_k[0] != 0) return fail(err, errlen, "cu_seqlens_k must start at 0");
@@ -151,6 +151,7 @@ bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int
     if ((int)ents.size() > max_blocks) return fail(err, errlen, "plan needs %zu blocks, room for %d", ents.size(), max_blocks);
     if (cu_q[n_seq] > max_tok) return fail(err, errlen, "plan needs %d tok_kv entries, room for %d", cu_q[n_seq], max_tok);
     if ((!blocks && !ents.empty()) || (!tok_kv && cu_q[n_seq])) return fail(err, errlen, "missing plan output arrays");
+    if (kv_tok && total_kv > max_kv) return fail(err, errlen, "plan needs %d kv_tok entries, room for %d", total_kv, max_kv);
     // Longest key range first, so the long causal blocks start early (clef_metal.m:1243-1257
     // orders each record's blocks longest first; here the order is global across records).
     std::stable_sort(ents.begin(), ents.end(), [](const Ent &x, const Ent &y) { return x.v[4] > y.v[4]; });
@@ -162,6 +163,10 @@ bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int
         const int k0 = cu_k ? cu_k[r] : kv_off;
         for (int j = 0; j < nq; j++) tok_kv[cu_q[r] + j] = k0 + (nk - nq) + j;
         if (!cu_k) kv_off += (nq + CLEF_HIP_KV_ALIGN - 1) / CLEF_HIP_KV_ALIGN * CLEF_HIP_KV_ALIGN;
+    }
+    if (kv_tok) {
+        for (int k = 0; k < total_kv; k++) kv_tok[k] = -1;
+        for (int t = 0; t < cu_q[n_seq]; t++) kv_tok[tok_kv[t]] = t;
     }
     *n_blk = (int)ents.size();
     *kv_rows = total_kv;
@@ -190,14 +195,14 @@ bool clef_hip_vis_positions(const int32_t *cu, int n_img, const int32_t *grid_w,
 
 bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {
     if (!check_text(a, false, err, errlen)) return false;
-    if (a->T == 0) return true;
+    if (a->T == 0 || a->kv_rows == 0) return true;
     PrepParams p;
     p.qkv = a->qkv; p.k_norm = a->k_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
-    p.tok_kv = a->tok_kv; p.k_plane = a->k_plane; p.vt_plane = a->vt_plane;
-    p.T = a->T; p.row = a->row; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
+    p.kv_tok = a->kv_tok; p.k_plane = a->k_plane; p.vt_plane = a->vt_plane;
+    p.kv_rows = a->kv_rows; p.row = a->row; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
     p.eps = a->eps; p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
-    dim3 grid((a->T + 15) / 16, a->nkv);
-    hipLaunchKernelGGL(text_prep_kv_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
+    dim3 grid((a->kv_rows + kPrepRows - 1) / kPrepRows, a->nkv);
+    hipLaunchKernelGGL(text_prep_kv_kernel, grid, dim3(16 * kPrepRows), 0, (hipStream_t)stream, p);
     return launch_ok("text_prep_kv", err, errlen);
 }
 

@@ -59,6 +59,35 @@ __device__ __forceinline__ float sigmoidf(float x) {
     return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
 }
 
+// sin and cos of a rotary angle (|x| < 2^20), without the memory tables of a general-range
+// routine. Cody-Waite reduction by pi/2 in three parts with fma (the parts come from the double
+// pi/2 split into floats), then Taylor polynomials on |r| <= pi/4: sin to r^9 (truncation
+// < 2e-9), cos to r^10 (< 1e-10); about 1-2 ulp overall for the float angle the caller formed.
+__device__ __forceinline__ void rope_sincos(float x, float *s, float *c) {
+    constexpr double kHalfPi = 1.5707963267948966;
+    constexpr float C1 = (float)kHalfPi;
+    constexpr float C2 = (float)(kHalfPi - (double)C1);
+    constexpr float C3 = (float)(kHalfPi - (double)C1 - (double)C2);
+    const float j = __builtin_rintf(x * 0.63661977236758134f);
+    float r = fmaf(-j, C1, x);
+    r = fmaf(-j, C2, r);
+    r = fmaf(-j, C3, r);
+    const float r2 = r * r;
+    float ps = fmaf(r2, 1.f / 362880.f, -1.f / 5040.f);
+    ps = fmaf(ps, r2, 1.f / 120.f);
+    ps = fmaf(ps, r2, -1.f / 6.f);
+    const float sr = fmaf(ps * r2, r, r);
+    float pc = fmaf(r2, -1.f / 3628800.f, 1.f / 40320.f);
+    pc = fmaf(pc, r2, -1.f / 720.f);
+    pc = fmaf(pc, r2, 1.f / 24.f);
+    pc = fmaf(pc, r2, -0.5f);
+    const float cr = fmaf(pc, r2, 1.f);
+    const int q = (int)j & 3;   // x = j pi/2 + r
+    const float sv = (q & 1) ? cr : sr, cv = (q & 1) ? sr : cr;
+    *s = (q & 2) ? -sv : sv;
+    *c = ((q + 1) & 2) ? -cv : cv;
+}
+
 __device__ __forceinline__ float wave_max_pair(float v) {
     return fmaxf(v, __shfl_xor(v, 32, 64));
 }
@@ -200,7 +229,7 @@ __global__ __launch_bounds__(256, 1) void attn_fwd_kernel(AttnParams p) {
                         const int ax = i % 3;
                         const float pos = ax == 0 ? pt : (ax == 1 ? ph : pw);
                         float sn, cs;
-                        sincosf(pos * fr[j], &sn, &cs);
+                        rope_sincos(pos * fr[j], &sn, &cs);
                         const float x0 = x[c][j], x1 = x[c + R][j];
                         x[c][j] = x0 * cs - x1 * sn;
                         x[c + R][j] = x1 * cs + x0 * sn;
@@ -536,101 +565,142 @@ __device__ __forceinline__ float row16_sum(float v) {   // sum over the lane's 1
     return v;
 }
 
-__global__ __launch_bounds__(256) void text_prep_kv_kernel(PrepParams p) {
-    constexpr int HD = 256, ROWS = 16;           // pass rows per workgroup
-    constexpr int VS = HD + 8;                   // LDS row stride of the V tile
-    __shared__ __attribute__((aligned(16))) uint16_t vr[ROWS * VS];
-    __shared__ int krows[ROWS];
-    const int tid = threadIdx.x;
-    const int c = tid & 31, rl = tid >> 5;       // 8-dim chunk of the row, row within a pass
-    const int t0 = blockIdx.x * ROWS, kh = blockIdx.y;
-    const int half_rot = p.n_rot / 2;   // 0 or 32: chunks 0-3 pair with chunks 4-7
-    // every global load is issued before the first use
+// K/V prologue over plane rows: workgroup (b, kh) owns plane rows 16b .. 16b+15 of kv head kh
+// and takes each row's key from pass row kv_tok[row] (-1: the row is left as it is). 16 lanes
+// per row, 16 dims per lane. K rows are normalised, rotated and stored whole (512 B per row).
+// V rows are staged row-major in LDS and read back transposed with ds_read_b64_tr_b16 (lane i
+// of a 16-lane group receives element i % 4 of the 8 bytes lane 4j + i / 4 addressed, for
+// j = 0..3), which hands each lane one head dim of 4 consecutive rows; two such reads make a
+// 16-byte V^T run of 8 plane rows. A run with rows the pass does not own (a prefix record's
+// cached rows, rows past a record) is merged with the plane's contents.
+constexpr int kPrepRows = 16;
+typedef short short4_t __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(16 * kPrepRows) void text_prep_kv_kernel(PrepParams p) {
+    constexpr int HD = 256, ROWS = kPrepRows, NT = 16 * ROWS;
+    constexpr int VS = HD + 64;   // LDS row stride: 4 rows' 128-byte reads fall in distinct banks
+    __shared__ __attribute__((aligned(16))) uint16_t vl[ROWS * VS];
+    __shared__ __attribute__((aligned(16))) float2 csl[ROWS][32];
+    __shared__ int trow[ROWS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rr = tid >> 4, k = tid & 15;       // row of the tile, 16-dim group of the row
+    const int r0 = blockIdx.x * ROWS, kh = blockIdx.y;
+    const int half_rot = p.n_rot / 2;            // 0 or 32: dims [0, 32) pair with [32, 64)
+    const int t = (r0 + rr < p.kv_rows) ? p.kv_tok[r0 + rr] : -1;
+    if (k == 0) trow[rr] = t;
+    if (!__syncthreads_or(t >= 0)) return;       // no row of this tile belongs to the pass
+    // global loads first
+    const uint16_t *src = p.qkv + (size_t)(t >= 0 ? t : 0) * p.row + (size_t)p.nh * 2 * HD + (size_t)kh * HD + 16 * k;
     u32x4 kw[2], vw[2];
-    int pos[2][8];
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
-        const int t = t0 + it * 8 + rl;
-        const bool ok = t < p.T;
-        const uint16_t *src = p.qkv + (size_t)(ok ? t : 0) * p.row + (size_t)p.nh * 2 * HD + (size_t)kh * HD + c * 8;
-        kw[it] = ok ? *(const u32x4 *)src : u32x4{0, 0, 0, 0};
-        vw[it] = ok ? *(const u32x4 *)(src + (size_t)p.nkv * HD) : u32x4{0, 0, 0, 0};
-        if (half_rot && c < 8) {
-            const int32_t *pp = p.pos3 + 3 * (size_t)(ok ? t : 0);
-#pragma unroll
-            for (int e = 0; e < 8; e++) pos[it][e] = pp[((c & 3) * 8 + e) % 3];
-        }
+    for (int h = 0; h < 2; h++) {
+        kw[h] = t >= 0 ? *(const u32x4 *)(src + 8 * h) : u32x4{0, 0, 0, 0};
+        vw[h] = t >= 0 ? *(const u32x4 *)(src + (size_t)p.nkv * HD + 8 * h) : u32x4{0, 0, 0, 0};
     }
-    if (tid < ROWS) krows[tid] = t0 + tid < p.T ? p.tok_kv[t0 + tid] : -1;
-    float wn[8], fr[8];
+    float wn[16];
     if (p.k_norm) {
-        const float4 w0 = *(const float4 *)(p.k_norm + c * 8), w1 = *(const float4 *)(p.k_norm + c * 8 + 4);
-        wn[0] = w0.x; wn[1] = w0.y; wn[2] = w0.z; wn[3] = w0.w; wn[4] = w1.x; wn[5] = w1.y; wn[6] = w1.z; wn[7] = w1.w;
-    }
-    if (half_rot && c < 8) {
-        const float4 f0 = *(const float4 *)(p.inv_freq + (c & 3) * 8), f1 = *(const float4 *)(p.inv_freq + (c & 3) * 8 + 4);
-        fr[0] = f0.x; fr[1] = f0.y; fr[2] = f0.z; fr[3] = f0.w; fr[4] = f1.x; fr[5] = f1.y; fr[6] = f1.z; fr[7] = f1.w;
-    }
-    __syncthreads();
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
-        const int rr = it * 8 + rl;
-        const int t = t0 + rr;
-        const int krow = krows[rr];
-        float x[8];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            x[2 * j] = bf_lo(kw[it][j]);
-            x[2 * j + 1] = bf_hi(kw[it][j]);
+        for (int q = 0; q < 4; q++) {
+            const float4 w4 = *(const float4 *)(p.k_norm + 16 * k + 4 * q);
+            wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
         }
-        if (p.k_norm) {
-            float ss = 0.f;
+    }
+    if (half_rot) {
+        // rotary table of the tile: ROWS x 32 pairs, pair i turns by axis i % 3
 #pragma unroll
-            for (int e = 0; e < 8; e++) ss += x[e] * x[e];
-            ss = row16_sum(ss);
-            ss += __shfl_xor(ss, 16, 64);
-            const float inv = rsqrtf(ss / (float)HD + p.eps);
-#pragma unroll
-            for (int e = 0; e < 8; e++) x[e] *= inv * wn[e];
-        }
-        if (half_rot) {
-            // partner chunk c ^ 4 (lanes 4 apart inside the 16-lane DPP row)
-            float y[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                // row_ror:n hands lane i the value of lane (i - n) mod 16
-                const float up = __builtin_amdgcn_update_dpp(0.f, x[e], 0x12c, 0xf, 0xf, false);   // lane + 4
-                const float dn = __builtin_amdgcn_update_dpp(0.f, x[e], 0x124, 0xf, 0xf, false);   // lane - 4
-                y[e] = (c & 4) ? dn : up;
-            }
-            if (c < 8 && t < p.T) {
-                const bool first = c < 4;
-                float *cs = p.rope_cs ? p.rope_cs + (size_t)t * 2 * half_rot : nullptr;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int i = (c & 3) * 8 + e;
-                    float sn, cn;
-                    sincosf((float)pos[it][e] * fr[e], &sn, &cn);
-                    x[e] = first ? x[e] * cn - y[e] * sn : x[e] * cn + y[e] * sn;
-                    if (cs && first) *(float2 *)(cs + 2 * i) = make_float2(cn, sn);
-                }
+        for (int j = 0; j < ROWS * 32 / NT; j++) {
+            const int idx = tid + NT * j, row = idx >> 5, i = idx & 31;
+            const int tt = trow[row];
+            if (tt >= 0) {
+                const float ang = (float)p.pos3[3 * (size_t)tt + i % 3] * p.inv_freq[i];
+                float sn, cn;
+                rope_sincos(ang, &sn, &cn);
+                csl[row][i] = make_float2(cn, sn);
+                if (p.rope_cs && kh == 0) *(float2 *)(p.rope_cs + (size_t)tt * 2 * half_rot + 2 * i) = make_float2(cn, sn);
             }
         }
-        if (krow >= 0) {
-            u32x4 ko = {pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7])};
-            *(u32x4 *)(p.k_plane + ((size_t)kh * p.kvT + krow) * HD + c * 8) = ko;
-        }
-        *(u32x4 *)(vr + rr * VS + c * 8) = vw[it];
     }
+    // V rows into LDS, row-major
+    *(u32x4 *)(vl + rr * VS + 16 * k) = vw[0];
+    *(u32x4 *)(vl + rr * VS + 16 * k + 8) = vw[1];
     __syncthreads();
-    // V^T: lane e of each 16-lane group writes row e's value of one dim (2 bytes); a group's
-    // 16 stores cover consecutive kv rows of one V^T row.
-    const int e = tid & 15;
-    const int krow = krows[e];
+    float x[16];
 #pragma unroll
-    for (int q = 0; q < HD / 16; q++) {
-        const int d = q * 16 + (tid >> 4);
-        if (krow >= 0) p.vt_plane[((size_t)kh * HD + d) * p.kvT + krow] = vr[e * VS + d];
+    for (int j = 0; j < 4; j++) {
+        x[2 * j] = bf_lo(kw[0][j]);
+        x[2 * j + 1] = bf_hi(kw[0][j]);
+        x[8 + 2 * j] = bf_lo(kw[1][j]);
+        x[8 + 2 * j + 1] = bf_hi(kw[1][j]);
+    }
+    if (p.k_norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) ss += x[e] * x[e];
+        ss = row16_sum(ss);
+        const float inv = rsqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+        for (int e = 0; e < 16; e++) x[e] *= inv * wn[e];
+    }
+    if (half_rot) {
+        // lanes 0, 1 hold dims 0-31, lanes 2, 3 their partners 32-63 (two lanes apart)
+        float y[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            // row_ror:n hands lane i the value of lane (i - n) mod 16
+            const float up = __builtin_amdgcn_update_dpp(0.f, x[e], 0x12e, 0xf, 0xf, false);   // lane + 2
+            const float dn = __builtin_amdgcn_update_dpp(0.f, x[e], 0x122, 0xf, 0xf, false);   // lane - 2
+            y[e] = (k & 2) ? dn : up;
+        }
+        if (k < 4) {
+            const bool first = k < 2;
+            const float2 *cs = csl[rr] + 16 * (k & 1);
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const float2 v = cs[e];
+                x[e] = first ? x[e] * v.x - y[e] * v.y : x[e] * v.x + y[e] * v.y;
+            }
+        }
+    }
+    if (t >= 0) {
+        uint16_t *dst = p.k_plane + ((size_t)kh * p.kvT + r0 + rr) * HD + 16 * k;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const float *xs = x + 8 * h;
+            u32x4 ko = {pack_bf16(xs[0], xs[1]), pack_bf16(xs[2], xs[3]), pack_bf16(xs[4], xs[5]), pack_bf16(xs[6], xs[7])};
+            *(u32x4 *)(dst + 8 * h) = ko;
+        }
+    }
+    // V^T: wave w covers dims 64(w%4) .. +63 of rows 16(w/4) .. +15. In read q (rows
+    // 16(w/4) + 4q .. +3), lane s of 16-lane group g addresses row 16(w/4) + 4q + s/4, dims
+    // 64(w%4) + 16g + 4(s%4) .. +3, and receives dim 64(w%4) + 16g + s of the 4 rows.
+    const int g = lane >> 4, s16 = lane & 15, db = wave & 3, rg = wave >> 2;
+    const int d = 64 * db + 16 * g + s16;
+    const unsigned base = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) uint16_t *)vl;
+    short4_t rd[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const unsigned a = base + 2u * (unsigned)((16 * rg + 4 * q + (s16 >> 2)) * VS + 64 * db + 16 * g + 4 * (s16 & 3));
+        rd[q] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)(uintptr_t)a);
+    }
+#pragma unroll
+    for (int run = 0; run < 2; run++) {
+        const int rb = 16 * rg + 8 * run;
+        unsigned own = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) own |= (trow[rb + e] >= 0 ? 1u : 0u) << e;
+        if (!own) continue;
+        const short4_t lo = rd[2 * run], hi = rd[2 * run + 1];
+        u32x4 w = {(unsigned)(uint16_t)lo[0] | ((unsigned)(uint16_t)lo[1] << 16), (unsigned)(uint16_t)lo[2] | ((unsigned)(uint16_t)lo[3] << 16),
+                   (unsigned)(uint16_t)hi[0] | ((unsigned)(uint16_t)hi[1] << 16), (unsigned)(uint16_t)hi[2] | ((unsigned)(uint16_t)hi[3] << 16)};
+        uint16_t *dst = p.vt_plane + ((size_t)kh * HD + d) * p.kvT + r0 + rb;
+        if (own != 0xffu) {   // keep the rows this pass does not own
+            const u32x4 old = *(const u32x4 *)dst;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const unsigned m = ((own >> (2 * j)) & 1u ? 0xffffu : 0u) | ((own >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
+                w[j] = (w[j] & m) | (old[j] & ~m);
+            }
+        }
+        *(u32x4 *)dst = w;
     }
 }
 
@@ -663,7 +733,7 @@ __global__ __launch_bounds__(256) void vis_prep_kernel(VisPrepParams p) {
             if (i >= HALF) break;
             const float ang = (float)p.pos2[2 * tok + (i < QUART ? 0 : 1)] * p.inv_freq[i < QUART ? i : i - QUART];
             float sn, cs;
-            sincosf(ang, &sn, &cs);
+            rope_sincos(ang, &sn, &cs);
 #pragma unroll
             for (int part = 0; part < 2; part++) {
                 const int base = part * E + h * HD;

@@ -30,11 +30,11 @@ struct PrepParams {
     const float *k_norm;
     const int32_t *pos3;
     const float *inv_freq;
-    const int32_t *tok_kv;    // kv row of each pass row
+    const int32_t *kv_tok;    // pass row of each plane row, -1: not written
     uint16_t *k_plane;
     uint16_t *vt_plane;
     float *rope_cs;
-    int T, row, nh, nkv, n_rot, kvT;
+    int kv_rows, row, nh, nkv, n_rot, kvT;
     float eps;
 };
 

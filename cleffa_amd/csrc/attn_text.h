@@ -280,7 +280,7 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
                         const int ax = i % 3;
                         const float pos = ax == 0 ? pt : (ax == 1 ? ph : pw);
                         float sn, cs;
-                        sincosf(pos * fr[j], &sn, &cs);
+                        rope_sincos(pos * fr[j], &sn, &cs);
                         const float x0 = x[c][j], x1 = x[c + R][j];
                         x[c][j] = x0 * cs - x1 * sn;
                         x[c + R][j] = x1 * cs + x0 * sn;

@@ -45,7 +45,8 @@ def _gen(device, seed):
 
 def text_inputs(lengths, nh, nkv, hd=256, n_rot=64, seed=0, device="cpu", norm=True,
                 outlier_frac=0.02, outlier_scale=8.0, positions=None):
-    """Fused qkv rows [T][2*nh*hd + 2*nkv*hd] (bf16), norm weights, pos3 and cu_seqlens."""
+    """Fused qkv rows [T][2*nh*hd + 2*nkv*hd] (bf16), norm weights, pos3 and cu_seqlens.
+    positions: [T] (one position per token) or [T][3] (temporal, row, column)."""
     T = int(sum(lengths))
     row = 2 * nh * hd + 2 * nkv * hd
     g = _gen(device, seed)
@@ -66,7 +67,10 @@ def text_inputs(lengths, nh, nkv, hd=256, n_rot=64, seed=0, device="cpu", norm=T
         k_norm = (1.0 + 0.1 * torch.randn((hd,), generator=g, device=device)).float()
     if positions is None:
         positions = np.concatenate([np.arange(n) for n in lengths]) if T else np.zeros(0)
-    pos3 = torch.from_numpy(np.repeat(np.asarray(positions, dtype=np.int32)[:, None], 3, axis=1).copy()).to(device)
+    positions = np.asarray(positions, dtype=np.int32)
+    if positions.ndim == 1:   # text tokens: the same position on all three M-RoPE axes
+        positions = np.repeat(positions[:, None], 3, axis=1)
+    pos3 = torch.from_numpy(np.ascontiguousarray(positions)).to(device)
     return {"qkv": qkv, "q_norm": q_norm, "k_norm": k_norm, "pos3": pos3,
             "cu_seqlens": cu_seqlens(lengths), "lengths": list(lengths), "nh": nh, "nkv": nkv,
             "hd": hd, "n_rot": n_rot, "row": row}

@@ -66,12 +66,14 @@ int clef_hip_attn_plan_max_blocks(int n_seq, int Tq);
  * cu_k[r] .. cu_k[r+1] (multiples of 8), its first cu_k[r+1]-cu_k[r]-(cu_q[r+1]-cu_q[r]) keys are
  * cached, and its queries are the last tokens. causal = 0 gives bidirectional attention within
  * each record (vision). Outputs: blocks [max_blocks][8] (sorted longest first), tok_kv
- * [max_tok >= cu_q[n_seq]] (the K/V plane row each pass row's key lands in), *n_blk, *kv_rows
- * (rows per head the K and V^T planes need: every record's first kv row plus its key count
- * rounded up to 64, since the attention kernel reads whole 64-key tiles). */
+ * [max_tok >= cu_q[n_seq]] (the K/V plane row each pass row's key lands in), kv_tok
+ * [max_kv >= *kv_rows] (the inverse: the pass row whose key each plane row takes, -1 for rows
+ * the pass does not write; NULL skips it), *n_blk, *kv_rows (rows per head the K and V^T
+ * planes need: every record's first kv row plus its key count rounded up to 64, since the
+ * attention kernel reads whole 64-key tiles). */
 bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int causal,
                         int32_t *blocks, int max_blocks, int32_t *tok_kv, int max_tok,
-                        int *n_blk, int *kv_rows, char *err, size_t errlen);
+                        int32_t *kv_tok, int max_kv, int *n_blk, int *kv_rows, char *err, size_t errlen);
 
 /* RoPE frequency table: inv_freq[j] = 1 / theta^(2j/n_rot) in f32, j < n_rot/2
  * (clef_metal.m:176-184 text, 186-192 vision with n_rot = hd/2 and theta = 10000). */
@@ -101,7 +103,7 @@ typedef struct {
     int kvT;                  /* rows per head of the planes: >= plan kv_rows, multiple of 8 */
     const int32_t *blocks;    /* device copy of the plan's blocks */
     int n_blk;
-    const int32_t *tok_kv;    /* device copy of the plan's tok_kv [T] */
+    const int32_t *kv_tok;    /* device copy of the plan's kv_tok [kv_rows] */
     int kv_rows;              /* the plan's kv_rows */
     int causal;               /* 1 for the text models */
     int gate;                 /* 1: multiply by sigmoid(gate) (Qwen3.5 gated attention) */
@@ -114,9 +116,9 @@ typedef struct {
                                  CLEF_PROFILE analogue (clef_metal.m:52-68) at workgroup grain */
 } clef_hip_attn_args;
 
-/* K/V prologue only: RMSNorm + rotary of each pass row's K into plane row tok_kv[t], V into the
- * V^T plane (attn_prep / attn_prep_split / attn_prep_prefix K and V parts,
- * metal/clef.metal:245-300, 657-707, 873-928). Other plane rows are not written. */
+/* K/V prologue only: RMSNorm + rotary of each pass row's K into its plane row (kv_tok), V into
+ * the V^T plane (attn_prep / attn_prep_split / attn_prep_prefix K and V parts,
+ * metal/clef.metal:245-300, 657-707, 873-928). Plane rows with kv_tok -1 are not written. */
 bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen);
 /* Attention core with the Q prologue and gate epilogue fused (attention_tu and the FP32
  * kernels, metal/clef.metal:316-654, 709-849, 930-1093). Reads the planes prep_kv wrote. */

@@ -37,7 +37,7 @@ def _args(**over):
     a.nh, a.nkv, a.hd, a.n_rot, a.eps, a.scale = 24, 4, 256, 64, 1e-6, 1 / 16
     a.T, a.row, a.kvT, a.n_blk, a.kv_rows = 8, 14336, 64, 1, 64
     fake = ctypes.c_void_p(1 << 20)   # aligned, never dereferenced: every case fails validation first
-    for f in ("qkv", "q_norm", "k_norm", "pos3", "inv_freq", "k_plane", "vt_plane", "blocks", "tok_kv", "out"):
+    for f in ("qkv", "q_norm", "k_norm", "pos3", "inv_freq", "k_plane", "vt_plane", "blocks", "kv_tok", "out"):
         setattr(a, f, fake)
     for k, v in over.items():
         setattr(a, k, v)

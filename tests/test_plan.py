@@ -40,6 +40,10 @@ def _check_plan(cu_q, cu_k, causal):
                 assert k0 % KV_ALIGN == 0
             else:
                 assert k0 == cu_k[r]
+    # plane row -> pass row: the exact inverse of tok_kv, -1 everywhere else
+    inv = np.full(plan.kv_rows, -1, np.int32)
+    inv[plan.tok_kv_host] = np.arange(T, dtype=np.int32)
+    np.testing.assert_array_equal(plan.kv_tok_host, inv)
     return plan
 
 
