@@ -22,7 +22,7 @@ struct AttnParams {
     float eps, scale_log2, f16_lim;
     int causal, gate, out_type, out_ld;
     int xcd_heads;            // nh / 8 when heads split evenly over the 8 XCDs, else 0
-    uint64_t *trace;          // NULL, or [grid][4] per-workgroup start, end, HW_ID, XCC_ID
+    uint64_t *trace;          // NULL, or [grid][8] per-workgroup start, end, HW_ID, XCC_ID, prologue end, loop end
 };
 
 struct PrepParams {

@@ -94,7 +94,7 @@ __device__ __forceinline__ void static_for(F &&f) {
 // One (query block, q head) work item.
 template <int NROT>
 __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, const int h,
-                                           uint16_t *smem) {
+                                           uint16_t *smem, float *qn_lds, uint64_t *tr) {
     using namespace text;
     static_assert(NROT % 64 == 0 && NROT <= HD, "rotary pairs must sit in one lane");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -197,25 +197,12 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     const unsigned va1 = vl + 2 * (vrow * BK + (((4 + g) ^ vx) * 8));
 
     const int n_tiles = (k_len + BK - 1) / BK;
-    // the first tile streams in while the Q prologue runs
-    if (n_tiles > 0) load_tiles(0, k0s, v0s);
-
     // ---- Q prologue: lane holds Q[my_q][c*32 + 8g + j], the B operand of chunk c.
+    // Every prologue load is issued before any of them is waited for: q_norm (one element per
+    // thread, staged in LDS), the row's rotary cos/sin, the Q row chunks, then the first tile.
     bf16x8 qf[NC];
     {
-        // every prologue load is issued before any of them is waited for
-        const uint16_t *src = p.qkv + qrow * p.row + (size_t)h * 2 * HD;
-        u32x4 qw[NC];
-#pragma unroll
-        for (int c = 0; c < NC; c++) qw[c] = q_valid ? *(const u32x4 *)(src + c * 32 + 8 * g) : u32x4{0, 0, 0, 0};
-        float4 wv[NC][2];
-        if (p.q_norm) {   // NULL: no q/k norm (plain SDPA operands)
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                wv[c][0] = *(const float4 *)(p.q_norm + c * 32 + 8 * g);
-                wv[c][1] = *(const float4 *)(p.q_norm + c * 32 + 8 * g + 4);
-            }
-        }
+        const float qn_v = (p.q_norm && tid < HD) ? p.q_norm[tid] : 0.f;
         constexpr int R = NROT / 64;
         float4 csv[R > 0 ? R : 1][4];
         if (NROT > 0 && p.rope_cs) {   // cos/sin written by the K/V prologue for this pass row
@@ -225,6 +212,16 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) csv[c][q4] = *(const float4 *)(cs + 2 * (c * 32 + 8 * g) + 4 * q4);
         }
+        const uint16_t *src = p.qkv + qrow * p.row + (size_t)h * 2 * HD;
+        u32x4 qw[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) qw[c] = q_valid ? *(const u32x4 *)(src + c * 32 + 8 * g) : u32x4{0, 0, 0, 0};
+        if (n_tiles > 0) load_tiles(0, k0s, v0s);
+        // The LDS store and reads of q_norm are issued as asm: the compiler would otherwise wait
+        // for the tile's global_load_lds fills (vmcnt(0)) before touching LDS.
+        const unsigned qn_addr = lds_addr((const uint16_t *)qn_lds);
+        if (tid < HD) asm volatile("ds_write_b32 %0, %1" : : "v"(qn_addr + 4u * tid), "v"(qn_v) : "memory");
+        asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
         float x[NC][8];
         float ss = 0.f;
 #pragma unroll
@@ -238,12 +235,17 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
             for (int j = 0; j < 8; j++) ss += x[c][j] * x[c][j];
         }
         ss = xrow_sum(ss);
-        if (p.q_norm) {
+        __builtin_amdgcn_s_barrier();   // q_norm staged
+        if (p.q_norm) {   // NULL: no q/k norm (plain SDPA operands)
             const float inv = rsqrtf(ss / (float)HD + p.eps);
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                const float wn[8] = {wv[c][0].x, wv[c][0].y, wv[c][0].z, wv[c][0].w,
-                                     wv[c][1].x, wv[c][1].y, wv[c][1].z, wv[c][1].w};
+                bf16x8 r0 = lds_read16<0>(qn_addr + 4u * (c * 32 + 8 * g));
+                bf16x8 r1 = lds_read16<16>(qn_addr + 4u * (c * 32 + 8 * g));
+                lds_wait<0>(r0);
+                lds_wait<0>(r1);
+                const float4 w0 = __builtin_bit_cast(float4, r0), w1 = __builtin_bit_cast(float4, r1);
+                const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
                 for (int j = 0; j < 8; j++) x[c][j] = x[c][j] * inv * wn[j];
             }
@@ -303,6 +305,7 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     const float sl2 = p.scale_log2;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (tr && tid == 0) tr[4] = wall_clock64();
     // Two tiles per trip: each call names its read and fill buffers statically.
     auto tile = [&](const int t, auto BUF) {
         constexpr int buf = decltype(BUF)::value;
@@ -407,6 +410,7 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
         if (t + 1 < n_tiles) tile(t + 1, std::integral_constant<int, 1>{});
     }
 
+    if (tr && tid == 0) tr[5] = wall_clock64();
     // ---- Epilogue: O / l times sigmoid(gate); lane (q16, g) holds dims 32u + 8g + [0, 8).
     // The gate rows were loaded into the buffers the last tile left idle.
     const uint16_t *gate0 = (n_tiles & 1) ? k1s : k0s, *gate1 = (n_tiles & 1) ? v1s : v0s;
@@ -442,6 +446,7 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
 template <int NROT>
 __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t smem[text::LDS_ELEMS];
+    __shared__ __attribute__((aligned(16))) float qn_lds[text::HD];
     uint64_t t0 = 0;
     if (p.trace && threadIdx.x == 0) t0 = wall_clock64();
     int bi, h;
@@ -456,16 +461,15 @@ __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
         bi = blockIdx.x / p.nh;
         h = blockIdx.x - bi * p.nh;
     }
-    text_block<NROT>(p, bi, h, smem);
-    if (p.trace && threadIdx.x == 0) {
-        // per-workgroup trace: start / end (100 MHz wall clock), hardware id, XCC id
-        const uint64_t t1 = wall_clock64();
-        const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
-        const unsigned xcc = __builtin_amdgcn_s_getreg((15 << 11) | 20);
-        p.trace[4 * blockIdx.x] = t0;
-        p.trace[4 * blockIdx.x + 1] = t1;
-        p.trace[4 * blockIdx.x + 2] = hw;
-        p.trace[4 * blockIdx.x + 3] = xcc;
+    uint64_t *tr = p.trace ? p.trace + 8 * blockIdx.x : nullptr;
+    text_block<NROT>(p, bi, h, smem, qn_lds, tr);
+    if (tr && threadIdx.x == 0) {
+        // per-workgroup trace (100 MHz wall clock): start, end, hardware id, XCC id; the block
+        // wrote the end of its prologue and of its key loop into slots 4 and 5
+        tr[0] = t0;
+        tr[1] = wall_clock64();
+        tr[2] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+        tr[3] = __builtin_amdgcn_s_getreg((15 << 11) | 20);
     }
 }
 
