@@ -43,7 +43,7 @@ class VisArgs(ctypes.Structure):
         ("P", c_int), ("heads", c_int), ("hd", c_int), ("scale", c_float),
         ("qkv", c_void_p), ("bias", c_void_p), ("pos2", c_void_p), ("inv_freq", c_void_p),
         ("q_plane", c_void_p), ("k_plane", c_void_p), ("vt_plane", c_void_p), ("kvT", c_int),
-        ("blocks", c_void_p), ("n_blk", c_int), ("tok_kv", c_void_p), ("kv_rows", c_int),
+        ("blocks", c_void_p), ("n_blk", c_int), ("kv_tok", c_void_p), ("kv_rows", c_int),
         ("out", c_void_p), ("out_type", c_int), ("f16_lim", c_float), ("ovf", c_void_p),
     ]
 

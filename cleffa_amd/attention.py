@@ -254,7 +254,6 @@ class TextAttention:
 class VisionAttention:
     """Vision tower attention: hd 72, MHA, bidirectional within each image, 2-D rotary."""
 
-    HDK = 80
 
     def __init__(self, heads=16, hd=72, theta=10000.0, device="cuda"):
         self.heads, self.hd = heads, hd
@@ -284,14 +283,14 @@ class VisionAttention:
         if scratch is None:
             scratch = self.scratch(P, kvT)
         q_plane, k_plane, vt_plane = scratch
-        _check(q_plane, "q_plane", (self.heads, P, self.HDK), torch.bfloat16, dev)
-        _check(k_plane, "k_plane", (self.heads, kvT, self.HDK), torch.bfloat16, dev)
+        _check(q_plane, "q_plane", (self.heads, P, self.hd), torch.bfloat16, dev)
+        _check(k_plane, "k_plane", (self.heads, kvT, self.hd), torch.bfloat16, dev)
         _check(vt_plane, "vt_plane", (self.heads, self.hd, kvT), torch.bfloat16, dev)
         a = VisArgs()
         a.P, a.heads, a.hd, a.scale = P, self.heads, self.hd, self.scale
         a.qkv, a.bias, a.pos2, a.inv_freq = _ptr(qkv), _ptr(bias), _ptr(pos2), _ptr(self.inv_freq)
         a.q_plane, a.k_plane, a.vt_plane, a.kvT = _ptr(q_plane), _ptr(k_plane), _ptr(vt_plane), kvT
-        a.blocks, a.n_blk, a.tok_kv, a.kv_rows = _ptr(plan.blocks), plan.n_blk, _ptr(plan.tok_kv), plan.kv_rows
+        a.blocks, a.n_blk, a.kv_tok, a.kv_rows = _ptr(plan.blocks), plan.n_blk, _ptr(plan.kv_tok), plan.kv_rows
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
         err = _err()
         _lib.check(lib.clef_hip_vis_attention(ctypes.byref(a), _stream_handle(stream), err, len(err)), err)
@@ -299,6 +298,6 @@ class VisionAttention:
 
     def scratch(self, P, kvT):
         dev = self.device
-        return (torch.empty((self.heads, max(P, 1), self.HDK), dtype=torch.bfloat16, device=dev),
-                torch.empty((self.heads, kvT, self.HDK), dtype=torch.bfloat16, device=dev),
+        return (torch.empty((self.heads, max(P, 1), self.hd), dtype=torch.bfloat16, device=dev),
+                torch.empty((self.heads, kvT, self.hd), dtype=torch.bfloat16, device=dev),
                 torch.empty((self.heads, self.hd, kvT), dtype=torch.bfloat16, device=dev))

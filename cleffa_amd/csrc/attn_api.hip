@@ -11,6 +11,7 @@
 
 #include "attn_kernels.h"
 #include "attn_text.h"
+#include "attn_vis.h"
 #include "attn_params.h"
 #include "clef_hip_attn.h"
 
@@ -19,7 +20,7 @@ using namespace clef_hip;
 namespace {
 
 constexpr int kVersion = 1;
-constexpr int kVisHD = 72, kVisHDK = 80;
+constexpr int kVisHD = 72;
 
 bool fail(char *err, size_t errlen, const char *fmt, ...) {
     if (err && errlen) {
@@ -246,13 +247,13 @@ bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err,
     if (!aligned16(a->q_plane) || !aligned16(a->k_plane) || !aligned16(a->vt_plane) || !aligned16(a->out))
         return fail(err, errlen, "vision planes and output must be 16-byte aligned");
     if (a->out_type < CLEF_HIP_OUT_BF16 || a->out_type > CLEF_HIP_OUT_F32) return fail(err, errlen, "bad out_type %d", a->out_type);
-    if ((a->n_blk && !a->blocks) || (a->P && !a->tok_kv)) return fail(err, errlen, "missing plan");
-    if (a->P) {
+    if ((a->n_blk && !a->blocks) || (a->kv_rows && !a->kv_tok)) return fail(err, errlen, "missing plan");
+    if (a->P && a->kv_rows) {
         VisPrepParams q;
-        q.qkv = a->qkv; q.bias = a->bias; q.pos2 = a->pos2; q.inv_freq = a->inv_freq; q.tok_kv = a->tok_kv;
+        q.qkv = a->qkv; q.bias = a->bias; q.pos2 = a->pos2; q.inv_freq = a->inv_freq; q.kv_tok = a->kv_tok;
         q.q_plane = a->q_plane; q.k_plane = a->k_plane; q.vt_plane = a->vt_plane;
-        q.P = a->P; q.heads = a->heads; q.kvT = a->kvT;
-        hipLaunchKernelGGL(vis_prep_kernel, dim3((a->P + 15) / 16, a->heads), dim3(256), 0, (hipStream_t)stream, q);
+        q.P = a->P; q.heads = a->heads; q.kvT = a->kvT; q.kv_rows = a->kv_rows;
+        hipLaunchKernelGGL(vis_prep_kernel, dim3((a->kv_rows + 15) / 16, a->heads), dim3(256), 0, (hipStream_t)stream, q);
         if (!launch_ok("vis_prep", err, errlen)) return false;
     }
     if (a->n_blk == 0) return true;
@@ -263,9 +264,8 @@ bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err,
     p.T = a->P; p.kvT = a->kvT; p.nh = a->heads; p.nkv = a->heads;
     p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = a->f16_lim;
     p.causal = 0; p.gate = 0; p.out_type = a->out_type; p.out_ld = a->heads * kVisHD;
-    (void)kVisHDK;
-    hipLaunchKernelGGL((attn_fwd_kernel<72, 64, false, 0, false, false>), dim3((unsigned)(a->n_blk * a->heads)), dim3(256), 0, (hipStream_t)stream, p);
-    return launch_ok("attn_fwd<72>", err, errlen);
+    hipLaunchKernelGGL(attn_vis_kernel, dim3((unsigned)(a->n_blk * a->heads)), dim3(512), 0, (hipStream_t)stream, p);
+    return launch_ok("attn_vis", err, errlen);
 }
 
 }  // extern "C"

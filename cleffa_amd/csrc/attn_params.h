@@ -12,7 +12,7 @@ struct AttnParams {
     const int32_t *pos3;
     const float *inv_freq;
     const float *rope_cs;     // text: cos/sin per pass row [T][n_rot/2][2], or NULL
-    const uint16_t *q_plane;  // vision: prepared Q [heads][T][HDK]
+    const uint16_t *q_plane;  // vision: prepared Q [heads][T][72]
     const uint16_t *k_plane;
     const uint16_t *vt_plane;
     const int32_t *blocks;
@@ -43,11 +43,11 @@ struct VisPrepParams {
     const float *bias;
     const int32_t *pos2;
     const float *inv_freq;
-    const int32_t *tok_kv;
+    const int32_t *kv_tok;    // patch of each plane row, -1: not written
     uint16_t *q_plane;
     uint16_t *k_plane;
     uint16_t *vt_plane;
-    int P, heads, kvT;
+    int P, heads, kvT, kv_rows;
 };
 
 }  // namespace clef_hip

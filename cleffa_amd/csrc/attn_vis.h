@@ -1,0 +1,260 @@
+// Vision tower attention for head dim 72 on CDNA4: bidirectional attention within each image
+// (metal/clef.metal:1720-1964, vis_attention_mma / _mpp), Q and K already biased and rotated
+// by the vision prologue. Same structure as the text kernel: 8 waves x 16 query rows,
+// S^T = K . Q^T and O^T += V^T . P^T with v_mfma_f32_16x16x32_bf16, K and V^T tiles of 64 keys
+// streamed global -> LDS with global_load_lds, double buffered, XOR-swizzled.
+// The 72-dim contraction runs as three 32-dim chunks: Q holds zeros in dims 72..95, and the
+// K slots of those dims hold copies of real K chunks of the same row (finite), so they add 0.
+// O^T covers 96 rows: V^T rows 72..95 of both LDS buffers are zeroed once per workgroup.
+#pragma once
+#include "attn_text.h"
+
+namespace clef_hip {
+namespace vis {
+constexpr int HD = 72;                 // head dim
+constexpr int ROWB = HD * 2;           // bytes per Q / K plane row (9 chunks of 16 bytes)
+constexpr int RCH = ROWB / 16;         // 16-byte chunks per plane row
+constexpr int NC = 3;                  // 32-dim chunks of the contraction (96 with padding)
+constexpr int NM = 6;                  // 16-row O^T tiles (96 rows)
+constexpr int HDV = 96;                // V^T rows in LDS
+constexpr int BQ = 128, BK = 64, WAVES = 8, ROWS = 16;
+constexpr int KSLOTS = 16;             // 16-byte slots per K row in LDS (12 carry data)
+constexpr int KTILE = BK * KSLOTS * 8; // elements per K tile (16 KB)
+constexpr int VTILE = HDV * BK;        // elements per V^T tile (12 KB)
+constexpr int LDS_ELEMS = 2 * KTILE + 2 * VTILE;
+}  // namespace vis
+
+__global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
+    using namespace vis;
+    using text::k_swz;
+    using text::s_row_key;
+    using text::lds_read16;
+    using text::lds_wait;
+    using text::lds_addr;
+    using text::static_for;
+    using text::xrow_max;
+    using text::xrow_sum;
+    typedef __attribute__((ext_vector_type(4))) float f32x4;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[LDS_ELEMS];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int q16 = lane & 15, g = lane >> 4;
+    const int bi = blockIdx.x / p.nh, h = blockIdx.x - bi * p.nh;
+    const int32_t *blk = p.blocks + 8 * bi;
+    const int q_row0 = blk[0], nq = blk[1], k_row0 = blk[3], k_len = blk[4];
+    const int flag_row = blk[5];
+    const int my_q = wave * ROWS + q16;
+    const bool q_valid = my_q < nq;
+    const bool wave_live = wave * ROWS < nq;
+    const size_t qrow = (size_t)q_row0 + (q_valid ? my_q : 0);
+
+    const uint16_t *kbase = p.k_plane + ((size_t)h * p.kvT + k_row0) * HD;
+    const uint16_t *vbase = p.vt_plane + (size_t)h * HD * p.kvT + k_row0;
+    uint16_t *const k0s = smem, *const k1s = smem + KTILE, *const v0s = smem + 2 * KTILE,
+                   *const v1s = smem + 2 * KTILE + VTILE;
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+
+    // K fills: slot s of a tile = key s/16, LDS slot s%16 holding logical chunk
+    // (s%16) ^ k_swz(key); logical chunks 9..15 are padding and take chunk (logical - 9).
+    // V^T fills: slot s = dim s/8, chunk (s%8) ^ v_swz(dim), 72 dims = 9 groups of 64 slots.
+    unsigned kfo[2], vfo[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int s = (wave_s * 2 + j) * 64 + lane;
+        const int key = s >> 4;
+        const int lc = (s & 15) ^ k_swz(key);
+        kfo[j] = (unsigned)(key * ROWB + (lc < RCH ? lc : lc - RCH) * 16);
+        const int grp = j == 0 ? wave_s : 8;
+        const int vs = grp * 64 + lane;
+        const int d = vs >> 3, c = (vs & 7) ^ text::v_swz(d);
+        vfo[j] = (unsigned)d * (unsigned)p.kvT * 2u + (unsigned)c * 16u;
+    }
+    auto load_tiles = [&](int kb, uint16_t *Ks, uint16_t *Vs) {
+        const char *kt_base = (const char *)(kbase + (size_t)kb * HD);
+        const char *vt_base = (const char *)(vbase + kb);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(kt_base + kfo[j]),
+                                             (lds_void *)(Ks + (wave_s * 2 + j) * 512), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[0]), (lds_void *)(Vs + wave_s * 512), 16, 0, 0);
+        if (wave_s == 0)
+            __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[1]), (lds_void *)(Vs + 8 * 512), 16, 0, 0);
+    };
+    auto zero_tail = [&](int kb, uint16_t *Vs) {   // V^T entries of keys >= k_len -> 0
+        const int valid = k_len - kb;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int s = tid + 512 * j;
+            if (s < HD * 8) {
+                const int d = s >> 3, c = (s & 7) ^ text::v_swz(d);
+                const int k0 = c * 8;
+                u32x4 w = *(u32x4 *)(Vs + s * 8);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const unsigned keep = (k0 + 2 * e + 1 < valid) ? 0xffffffffu : (k0 + 2 * e < valid ? 0xffffu : 0u);
+                    w[e] &= keep;
+                }
+                *(u32x4 *)(Vs + s * 8) = w;
+            }
+        }
+    };
+
+    // per-lane LDS byte addresses of the A operands
+    const unsigned kl = lds_addr(smem), vl = kl + 2 * 2 * KTILE;
+    unsigned ka[4][NC];
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+        const int key = s_row_key(kt, q16);
+        const int x = k_swz(key);
+#pragma unroll
+        for (int c = 0; c < NC; c++) ka[kt][c] = kl + 16 * (key * KSLOTS + ((4 * c + g) ^ x));
+    }
+    const int vrow = 8 * (q16 >> 2) + (q16 & 3);   // + 32*(mt>>1) + 4*(mt&1)
+    const int vx = text::v_swz(vrow);
+    const unsigned va0 = vl + 2 * (vrow * BK + ((g ^ vx) * 8));
+    const unsigned va1 = vl + 2 * (vrow * BK + (((4 + g) ^ vx) * 8));
+
+    const int n_tiles = (k_len + BK - 1) / BK;
+    // V^T rows 72..95 of both buffers stay zero
+    for (int i = tid; i < 2 * (HDV - HD) * BK / 8; i += 512) {
+        const int b = i / ((HDV - HD) * BK / 8), r = i % ((HDV - HD) * BK / 8);
+        *(u32x4 *)((b ? v1s : v0s) + HD * BK + r * 8) = u32x4{0, 0, 0, 0};
+    }
+    if (n_tiles > 0) load_tiles(0, k0s, v0s);
+
+    // ---- Q: lane holds Q[my_q][32c + 8g + j] (zero past dim 72), the B operand of chunk c.
+    bf16x8 qf[NC];
+    {
+        const uint16_t *src = p.q_plane + ((size_t)h * p.T + qrow) * HD;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int ch = 4 * c + g;
+            const u32x4 w = (q_valid && ch < RCH) ? *(const u32x4 *)(src + ch * 8) : u32x4{0, 0, 0, 0};
+            qf[c] = __builtin_bit_cast(bf16x8, w);
+        }
+    }
+    f32x4 o[NM];
+#pragma unroll
+    for (int mt = 0; mt < NM; mt++) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+    const float sl2 = p.scale_log2;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    auto tile = [&](const int t, auto BUF) {
+        constexpr int buf = decltype(BUF)::value;
+        uint16_t *const Vs = buf ? v1s : v0s, *const Kn = buf ? k0s : k1s, *const Vn = buf ? v0s : v1s;
+        const int kb = t * BK;
+        if (kb + BK > k_len) {   // WG-uniform: the block's last tile
+            zero_tail(kb, Vs);
+            __syncthreads();
+        }
+        if (t + 1 < n_tiles) load_tiles(kb + BK, Kn, Vn);
+        if (wave_live) {
+            constexpr int DEPTH = 6, QK = 4 * NC;
+            f32x4 s[4];
+            bf16x8 ring[DEPTH];
+            static_for<DEPTH>([&](auto I) {
+                constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
+                ring[st] = lds_read16<buf * 2 * KTILE>(ka[kt][c]);
+            });
+            static_for<QK>([&](auto I) {
+                constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
+                constexpr int ahead = (QK - 1 - st) < (DEPTH - 1) ? (QK - 1 - st) : (DEPTH - 1);
+                bf16x8 a = ring[st % DEPTH];
+                lds_wait<ahead>(a);
+                if constexpr (c == 0) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[kt], 0, 0, 0);
+                if constexpr (st + DEPTH < QK) {
+                    constexpr int n = st + DEPTH, nkt = n & 3, nc = n >> 2;
+                    ring[st % DEPTH] = lds_read16<buf * 2 * KTILE>(ka[nkt][nc]);
+                }
+            });
+            constexpr int PV = NM * 2;
+            auto vread = [&](auto I) {   // step st = NM * kc + mt
+                constexpr int st = decltype(I)::value, mt = st % NM, kc = st / NM;
+                constexpr int off = buf * 2 * VTILE + (32 * (mt >> 1) + 4 * (mt & 1)) * BK * 2;
+                return lds_read16<off>(kc ? va1 : va0);
+            };
+            bf16x8 vring[DEPTH];
+            static_for<DEPTH>([&](auto I) { vring[decltype(I)::value] = vread(I); });
+            if (kb + BK > k_len) {
+                // element (kt, i) is key kb + 32(kt>>1) + 8g + 4(kt&1) + i
+                const int lim = k_len - 1 - kb - 8 * g;
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        s[kt][i] = (32 * (kt >> 1) + 4 * (kt & 1) + i > lim) ? -INFINITY : s[kt][i];
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kt][i]);
+            mx = xrow_max(mx) * sl2;
+            const float mn = fmaxf(m_run, mx);
+            const float msub = (mn == -INFINITY) ? 0.f : mn;
+            const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
+            float rs = 0.f;
+            bf16x8 pk[2];
+#pragma unroll
+            for (int kc = 0; kc < 2; kc++) {
+                unsigned w[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int kt = 2 * kc + (j >> 1), i = 2 * (j & 1);
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][i], sl2, -msub));
+                    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][i + 1], sl2, -msub));
+                    w[j] = pack_bf16(p0, p1);
+                    rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]),
+                                                         bf16x2{(__bf16)1.0f, (__bf16)1.0f}, rs, false);
+                }
+                u32x4 wv = {w[0], w[1], w[2], w[3]};
+                pk[kc] = __builtin_bit_cast(bf16x8, wv);
+            }
+            rs = xrow_sum(rs);
+            l_run = l_run * alpha + rs;
+            m_run = mn;
+            if (__any(alpha != 1.f)) {
+#pragma unroll
+                for (int mt = 0; mt < NM; mt++) o[mt] *= alpha;
+            }
+            static_for<PV>([&](auto I) {
+                constexpr int st = decltype(I)::value, mt = st % NM, kc = st / NM;
+                constexpr int ahead = (PV - 1 - st) < (DEPTH - 1) ? (PV - 1 - st) : (DEPTH - 1);
+                bf16x8 a = vring[st % DEPTH];
+                lds_wait<ahead>(a);
+                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[kc], o[mt], 0, 0, 0);
+                if constexpr (st + DEPTH < PV) vring[st % DEPTH] = vread(std::integral_constant<int, st + DEPTH>{});
+            });
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+        tile(t, std::integral_constant<int, 0>{});
+        if (t + 1 < n_tiles) tile(t + 1, std::integral_constant<int, 1>{});
+    }
+
+    // ---- Epilogue: O / l; lane (q16, g) holds dims 32u + 8g + [0, 8) (stored below dim 72)
+    if (q_valid) {
+        const float il = l_run > 0.f ? 1.f / l_run : 0.f;
+        const size_t t = (size_t)q_row0 + my_q;
+        int32_t *flag = p.ovf ? p.ovf + flag_row : nullptr;
+#pragma unroll
+        for (int u = 0; u < NC; u++) {
+            const int d0 = 32 * u + 8 * g;
+            if (d0 >= HD) continue;
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[i] = o[2 * u][i] * il;
+                v[4 + i] = o[2 * u + 1][i] * il;
+            }
+            store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);
+        }
+    }
+}
+
+}  // namespace clef_hip

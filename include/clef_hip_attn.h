@@ -135,13 +135,13 @@ typedef struct {
     const float *bias;        /* [3*heads*hd] f32 or NULL */
     const int32_t *pos2;      /* [P][2] grid (row, column) per patch */
     const float *inv_freq;    /* [hd/4] */
-    uint16_t *q_plane;        /* [heads][P][80] scratch */
-    uint16_t *k_plane;        /* [heads][kvT][80] scratch */
-    uint16_t *vt_plane;       /* [heads][hd][kvT] scratch */
-    int kvT;
-    const int32_t *blocks;
+    uint16_t *q_plane;        /* [heads][P][72] scratch: biased, rotated Q */
+    uint16_t *k_plane;        /* [heads][kvT][72] scratch: biased, rotated K */
+    uint16_t *vt_plane;       /* [heads][72][kvT] scratch: biased V, transposed */
+    int kvT;                  /* >= the plan's kv_rows, multiple of 8 */
+    const int32_t *blocks;    /* device copy of a bidirectional plan's blocks */
     int n_blk;
-    const int32_t *tok_kv;
+    const int32_t *kv_tok;    /* device copy of the plan's kv_tok [kv_rows] */
     int kv_rows;
     void *out;                /* [P][heads*hd] */
     int out_type;
