@@ -266,56 +266,79 @@ __global__ __launch_bounds__(256) void vis_prep_kernel(VisPrepParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t qo[ROWS][HD], ko[ROWS][HD];
     __shared__ __attribute__((aligned(16))) uint16_t vt[HD * VS];
     __shared__ int trow[ROWS];
+    __shared__ float ang_pos[ROWS][2];
     const int tid = threadIdx.x, rr = tid >> 4, k = tid & 15;
     const int r0 = blockIdx.x * ROWS, h = blockIdx.y;
     const int E = p.heads * HD;
+    // loads that do not depend on the row's patch go first: the lane's bias chunks and the
+    // rotary frequencies of the pairs it turns
+    float bv[2][8];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int id = k + 16 * r;
+        if (id < 3 * CH && p.bias) {
+            const int part = id / CH, ch = id % CH;
+            const float *bb = p.bias + (size_t)part * E + (size_t)h * HD + ch * 8;
+            const float4 b0 = *(const float4 *)bb, b1 = *(const float4 *)(bb + 4);
+            bv[r][0] = b0.x; bv[r][1] = b0.y; bv[r][2] = b0.z; bv[r][3] = b0.w;
+            bv[r][4] = b1.x; bv[r][5] = b1.y; bv[r][6] = b1.z; bv[r][7] = b1.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) bv[r][j] = 0.f;
+        }
+    }
+    float fr[3];
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+        const int i = (tid + 256 * r) % HALF;
+        fr[r] = p.inv_freq[i < QUART ? i : i - QUART];
+    }
     const int t = (r0 + rr < p.kv_rows) ? p.kv_tok[r0 + rr] : -1;
     if (k == 0) trow[rr] = t;
     if (!__syncthreads_or(t >= 0)) return;
-    // loads: 27 chunks (q, k, v) per row over 16 lanes, bias added in float
+    // the row's 27 chunks (q, k, v) over 16 lanes, bias added in float; its grid position
     if (t >= 0) {
         const uint16_t *row = p.qkv + (size_t)t * 3 * E + (size_t)h * HD;
+        u32x4 w[2];
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int id = k + 16 * r;
+            if (id < 3 * CH) w[r] = *(const u32x4 *)(row + (size_t)(id / CH) * E + (id % CH) * 8);
+        }
+        if (k < 2) ang_pos[rr][k] = (float)p.pos2[2 * (size_t)t + k];
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int id = k + 16 * r;
             if (id < 3 * CH) {
                 const int part = id / CH, ch = id % CH;
-                const u32x4 w = *(const u32x4 *)(row + (size_t)part * E + ch * 8);
-                float v[8];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    v[2 * j] = bf_lo(w[j]);
-                    v[2 * j + 1] = bf_hi(w[j]);
+                    xs[rr][part][ch * 8 + 2 * j] = bf_lo(w[r][j]) + bv[r][2 * j];
+                    xs[rr][part][ch * 8 + 2 * j + 1] = bf_hi(w[r][j]) + bv[r][2 * j + 1];
                 }
-                if (p.bias) {
-                    const float *bb = p.bias + (size_t)part * E + (size_t)h * HD + ch * 8;
-#pragma unroll
-                    for (int j = 0; j < 8; j++) v[j] += bb[j];
-                }
-#pragma unroll
-                for (int j = 0; j < 8; j++) xs[rr][part][ch * 8 + j] = v[j];
             }
         }
     }
     __syncthreads();
     // rotary: one lane per (row, pair); V goes to the transposed LDS tile
-    for (int id = tid; id < ROWS * HALF; id += 256) {
-        const int r = id / HALF, i = id % HALF;
-        const int tt = trow[r];
-        if (tt < 0) continue;
-        const float ang = (float)p.pos2[2 * (size_t)tt + (i < QUART ? 0 : 1)] * p.inv_freq[i < QUART ? i : i - QUART];
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+        const int id = tid + 256 * r;
+        if (id >= ROWS * HALF) break;
+        const int row = id / HALF, i = id % HALF;
+        if (trow[row] < 0) continue;
         float sn, cs;
-        rope_sincos(ang, &sn, &cs);
-        const float q0 = xs[r][0][i], q1 = xs[r][0][i + HALF];
-        const float k0 = xs[r][1][i], k1 = xs[r][1][i + HALF];
-        qo[r][i] = f2bf(q0 * cs - q1 * sn);
-        qo[r][i + HALF] = f2bf(q1 * cs + q0 * sn);
-        ko[r][i] = f2bf(k0 * cs - k1 * sn);
-        ko[r][i + HALF] = f2bf(k1 * cs + k0 * sn);
+        rope_sincos(ang_pos[row][i < QUART ? 0 : 1] * fr[r], &sn, &cs);
+        const float q0 = xs[row][0][i], q1 = xs[row][0][i + HALF];
+        const float k0 = xs[row][1][i], k1 = xs[row][1][i + HALF];
+        qo[row][i] = f2bf(q0 * cs - q1 * sn);
+        qo[row][i + HALF] = f2bf(q1 * cs + q0 * sn);
+        ko[row][i] = f2bf(k0 * cs - k1 * sn);
+        ko[row][i + HALF] = f2bf(k1 * cs + k0 * sn);
     }
     for (int id = tid; id < ROWS * HD; id += 256) {
-        const int r = id / HD, d = id % HD;
-        vt[d * VS + r] = f2bf(xs[r][2][d]);
+        const int row = id / HD, d = id % HD;
+        vt[d * VS + row] = f2bf(xs[row][2][d]);
     }
     __syncthreads();
     // Q and K rows: 9 chunks each

@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from cleffa_amd import AttnPlan, TextAttention, VisionAttention, rope_inv_freq, workloads
+from cleffa_amd import AttnPlan, TextAttention, VisionAttention, rope_inv_freq, vision_positions, workloads
 from oracle import oracle
 from tests.helpers import assert_close, gpu_text, oracle_text
 
@@ -217,3 +217,25 @@ def test_rope_table_accuracy():
     got = cs.cpu().numpy()
     assert np.abs(got[..., 0] - np.cos(ang)).max() <= 2e-7
     assert np.abs(got[..., 1] - np.sin(ang)).max() <= 2e-7
+
+
+def test_vision_mixed_images_and_f16():
+    """Images of different grids (2x2, 4x6, 6x10, 16x18: patch counts that are not multiples of
+    16 or 64), no bias, bf16 and f16 outputs, against the float64 oracle."""
+    _say("[parity] vision mixed grids")
+    grids = [(2, 2), (4, 6), (6, 10), (16, 18)]
+    heads, hd = 4, 72
+    lens = [a * b for a, b in grids]
+    P = sum(lens)
+    g = torch.Generator().manual_seed(21)
+    qkv = torch.randn((P, 3 * heads * hd), generator=g).to(torch.bfloat16)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    pos2 = vision_positions(cu, [b for _, b in grids], 2)
+    vis = VisionAttention(heads, hd)
+    plan = AttnPlan(cu, causal=False)
+    Q, K, V = oracle.vis_prep(qkv.float().numpy(), heads, hd, None, pos2, rope_inv_freq(10000.0, hd // 2))
+    want = oracle.attention(Q, K, V, cu, None, False, hd ** -0.5, None)
+    for dt in ("bf16", "f16"):
+        out = vis.forward(qkv.cuda(), None, torch.from_numpy(pos2).cuda(), plan, out_dtype=dt)
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), want, what=f"vision {dt}")
