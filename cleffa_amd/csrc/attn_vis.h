@@ -193,7 +193,9 @@ __global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kt][i]);
             mx = xrow_max(mx) * sl2;
-            const float mn = fmaxf(m_run, mx);
+            // The running max moves only when a tile's max passes it by more than 8 (log2 units):
+            // P stays below 2^8, and the O rescale below runs on few tiles.
+            const float mn = (mx > m_run + 8.f) ? mx : m_run;
             const float msub = (mn == -INFINITY) ? 0.f : mn;
             const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
             float rs = 0.f;
