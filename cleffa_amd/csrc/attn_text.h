@@ -149,9 +149,10 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
             __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[j]),
                                              (lds_void *)(Vs + (wave_s * 4 + j) * 512), 16, 0, 0);
     };
-    // Gate rows of the block (128 x 256 bf16 = 64 KB): rows 0-63 into G0, 64-127 into G1, slot
-    // s of a half = row s/32, 16-byte chunk (s%32) ^ (row & 15).
-    auto load_gate = [&](uint16_t *G0, uint16_t *G1) {
+    // Q or gate rows of the block (128 x 256 bf16 = 64 KB, `off` 0 or HD within the head's
+    // 2*HD columns): rows 0-63 into G0, 64-127 into G1, slot s of a half = row s/32, 16-byte
+    // chunk (s%32) ^ (row & 15).
+    auto load_rows = [&](uint16_t *G0, uint16_t *G1, const int off) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int grp = wave * 8 + j;   // 64-slot group, 0..63
@@ -160,7 +161,7 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
             int rc = min(row, nq - 1);
             asm volatile("" : "+v"(rc));   // keeps the address math here, not hoisted out of the tile loop
             uint16_t *dst = (grp < 32 ? G0 : G1) + (grp & 31) * 512;
-            __builtin_amdgcn_global_load_lds((const void *)(p.qkv + ((size_t)q_row0 + rc) * p.row + (size_t)h * 2 * HD + HD + c * 8),
+            __builtin_amdgcn_global_load_lds((const void *)(p.qkv + ((size_t)q_row0 + rc) * p.row + (size_t)h * 2 * HD + off + c * 8),
                                              (lds_void *)dst, 16, 0, 0);
         }
     };
@@ -212,16 +213,23 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) csv[c][q4] = *(const float4 *)(cs + 2 * (c * 32 + 8 * g) + 4 * q4);
         }
-        const uint16_t *src = p.qkv + qrow * p.row + (size_t)h * 2 * HD;
-        u32x4 qw[NC];
-#pragma unroll
-        for (int c = 0; c < NC; c++) qw[c] = q_valid ? *(const u32x4 *)(src + c * 32 + 8 * g) : u32x4{0, 0, 0, 0};
+        // The block's Q rows go to buffers 1 by DMA (1 KB per instruction, where per-lane loads
+        // of the B-operand chunks would touch 16 rows each); buffers 1 stay free until the first
+        // tile issues the second tile's fills, after this prologue's closing barrier.
+        load_rows(k1s, v1s, 0);
         if (n_tiles > 0) load_tiles(0, k0s, v0s);
         // The LDS store and reads of q_norm are issued as asm: the compiler would otherwise wait
         // for the tile's global_load_lds fills (vmcnt(0)) before touching LDS.
         const unsigned qn_addr = lds_addr((const uint16_t *)qn_lds);
         if (tid < HD) asm volatile("ds_write_b32 %0, %1" : : "v"(qn_addr + 4u * tid), "v"(qn_v) : "memory");
-        asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_s_barrier();   // Q rows, q_norm and the first tile are in LDS
+        u32x4 qw[NC];
+        {
+            const uint16_t *qr = (my_q < 64 ? k1s : v1s) + (my_q & 63) * 256;
+#pragma unroll
+            for (int c = 0; c < NC; c++) qw[c] = *(const u32x4 *)(qr + (((4 * c + g) ^ (my_q & 15)) * 8));
+        }
         float x[NC][8];
         float ss = 0.f;
 #pragma unroll
@@ -235,7 +243,6 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
             for (int j = 0; j < 8; j++) ss += x[c][j] * x[c][j];
         }
         ss = xrow_sum(ss);
-        __builtin_amdgcn_s_barrier();   // q_norm staged
         if (p.q_norm) {   // NULL: no q/k norm (plain SDPA operands)
             const float inv = rsqrtf(ss / (float)HD + p.eps);
 #pragma unroll
@@ -316,7 +323,7 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
             __syncthreads();
         }
         if (t + 1 < n_tiles) load_tiles(kb + BK, Kn, Vn);
-        else if (p.gate) load_gate(Kn, Vn);   // the idle buffers take the epilogue's gate rows
+        else if (p.gate) load_rows(Kn, Vn, HD);   // the idle buffers take the epilogue's gate rows
         if (wave_live && (!p.causal || kb <= wave_last_pos)) {
             // S^T: 32 MFMAs (4 key tiles x 8 dim chunks), chunk-major so consecutive products
             // go to different accumulators. K operands are read DEPTH steps ahead of their
