@@ -264,7 +264,7 @@ bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err,
     p.T = a->P; p.kvT = a->kvT; p.nh = a->heads; p.nkv = a->heads;
     p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = a->f16_lim;
     p.causal = 0; p.gate = 0; p.out_type = a->out_type; p.out_ld = a->heads * kVisHD;
-    hipLaunchKernelGGL(attn_vis_kernel, dim3((unsigned)(a->n_blk * a->heads)), dim3(512), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(attn_vis_kernel, dim3((unsigned)(a->n_blk * a->heads)), dim3(64 * vis::WAVES), 0, (hipStream_t)stream, p);
     return launch_ok("attn_vis", err, errlen);
 }
 

@@ -371,10 +371,15 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kt][i]);
-            mx = xrow_max(mx) * sl2;
             // The running max moves only when a tile's max passes it by more than 8 (log2 units):
-            // P stays below 2^8, and the O rescale below runs on few tiles.
-            const float mn = (mx > m_run + 8.f) ? mx : m_run;
+            // P stays below 2^8, and the O rescale below runs on few tiles. The lane's own max
+            // decides whether any row of the wave may move; only then is the row max reduced
+            // over the row's four lanes.
+            float mn = m_run;
+            if (__any(mx * sl2 > m_run + 8.f)) {
+                const float rmx = xrow_max(mx) * sl2;
+                mn = (rmx > m_run + 8.f) ? rmx : m_run;
+            }
             const float msub = (mn == -INFINITY) ? 0.f : mn;
             const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
             float rs = 0.f;
@@ -395,8 +400,7 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
                 u32x4 wv = {w[0], w[1], w[2], w[3]};
                 pk[kc] = __builtin_bit_cast(bf16x8, wv);
             }
-            rs = xrow_sum(rs);
-            l_run = l_run * alpha + rs;
+            l_run = l_run * alpha + rs;   // the lane's share; the row's four lanes add up at the end
             m_run = mn;
             if (__any(alpha != 1.f)) {
 #pragma unroll
@@ -423,8 +427,9 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     // ---- Epilogue: O / l times sigmoid(gate); lane (q16, g) holds dims 32u + 8g + [0, 8).
     // The gate rows were loaded into the buffers the last tile left idle.
     const uint16_t *gate0 = (n_tiles & 1) ? k1s : k0s, *gate1 = (n_tiles & 1) ? v1s : v0s;
+    const float l_row = xrow_sum(l_run);   // outside the row-divergent branch: lanes exchange values
     if (q_valid) {
-        const float il = l_run > 0.f ? 1.f / l_run : 0.f;
+        const float il = l_row > 0.f ? 1.f / l_row : 0.f;
         const size_t t = (size_t)q_row0 + my_q;
         int32_t *flag = p.ovf ? p.ovf + flag_row : nullptr;
 #pragma unroll

@@ -1,8 +1,11 @@
 // Vision tower attention for head dim 72 on CDNA4: bidirectional attention within each image
 // (metal/clef.metal:1720-1964, vis_attention_mma / _mpp), Q and K already biased and rotated
-// by the vision prologue. Same structure as the text kernel: 8 waves x 16 query rows,
-// S^T = K . Q^T and O^T += V^T . P^T with v_mfma_f32_16x16x32_bf16, K and V^T tiles of 64 keys
-// streamed global -> LDS with global_load_lds, double buffered, XOR-swizzled.
+// by the vision prologue. Same data flow as the text kernel (S^T = K . Q^T and
+// O^T += V^T . P^T with v_mfma_f32_16x16x32_bf16, K and V^T tiles of 64 keys streamed
+// global -> LDS with global_load_lds, double buffered, XOR-swizzled), but 4 waves of 32 query
+// rows: each LDS operand read feeds the products of both 16-row halves, and the two halves'
+// softmax chains interleave. The small head dim leaves room for both halves' registers at two
+// workgroups per CU.
 // The 72-dim contraction runs as three 32-dim chunks: Q holds zeros in dims 72..95, and the
 // K slots of those dims hold copies of real K chunks of the same row (finite), so they add 0.
 // O^T covers 96 rows: V^T rows 72..95 of both LDS buffers are zeroed once per workgroup.
@@ -17,14 +20,14 @@ constexpr int RCH = ROWB / 16;         // 16-byte chunks per plane row
 constexpr int NC = 3;                  // 32-dim chunks of the contraction (96 with padding)
 constexpr int NM = 6;                  // 16-row O^T tiles (96 rows)
 constexpr int HDV = 96;                // V^T rows in LDS
-constexpr int BQ = 128, BK = 64, WAVES = 8, ROWS = 16;
+constexpr int BQ = 128, BK = 64, WAVES = 4, ROWS = 32;
 constexpr int KSLOTS = 16;             // 16-byte slots per K row in LDS (12 carry data)
 constexpr int KTILE = BK * KSLOTS * 8; // elements per K tile (16 KB)
 constexpr int VTILE = HDV * BK;        // elements per V^T tile (12 KB)
 constexpr int LDS_ELEMS = 2 * KTILE + 2 * VTILE;
 }  // namespace vis
 
-__global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
     using namespace vis;
     using text::k_swz;
     using text::s_row_key;
@@ -43,10 +46,7 @@ __global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
     const int32_t *blk = p.blocks + 8 * bi;
     const int q_row0 = blk[0], nq = blk[1], k_row0 = blk[3], k_len = blk[4];
     const int flag_row = blk[5];
-    const int my_q = wave * ROWS + q16;
-    const bool q_valid = my_q < nq;
     const bool wave_live = wave * ROWS < nq;
-    const size_t qrow = (size_t)q_row0 + (q_valid ? my_q : 0);
 
     const uint16_t *kbase = p.k_plane + ((size_t)h * p.kvT + k_row0) * HD;
     const uint16_t *vbase = p.vt_plane + (size_t)h * HD * p.kvT + k_row0;
@@ -56,15 +56,20 @@ __global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
 
     // K fills: slot s of a tile = key s/16, LDS slot s%16 holding logical chunk
     // (s%16) ^ k_swz(key); logical chunks 9..15 are padding and take chunk (logical - 9).
-    // V^T fills: slot s = dim s/8, chunk (s%8) ^ v_swz(dim), 72 dims = 9 groups of 64 slots.
-    unsigned kfo[2], vfo[2];
+    // Wave w fills K slot groups 4w .. 4w+3. V^T fills: slot s = dim s/8, chunk
+    // (s%8) ^ v_swz(dim), 72 dims = 9 groups of 64 slots: wave w fills groups 2w, 2w+1, and wave
+    // 0 also group 8.
+    unsigned kfo[4], vfo[3];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int s = (wave_s * 2 + j) * 64 + lane;
+    for (int j = 0; j < 4; j++) {
+        const int s = (wave_s * 4 + j) * 64 + lane;
         const int key = s >> 4;
         const int lc = (s & 15) ^ k_swz(key);
         kfo[j] = (unsigned)(key * ROWB + (lc < RCH ? lc : lc - RCH) * 16);
-        const int grp = j == 0 ? wave_s : 8;
+    }
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const int grp = j < 2 ? wave_s * 2 + j : 8;
         const int vs = grp * 64 + lane;
         const int d = vs >> 3, c = (vs & 7) ^ text::v_swz(d);
         vfo[j] = (unsigned)d * (unsigned)p.kvT * 2u + (unsigned)c * 16u;
@@ -73,18 +78,20 @@ __global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
         const char *kt_base = (const char *)(kbase + (size_t)kb * HD);
         const char *vt_base = (const char *)(vbase + kb);
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 4; j++)
             __builtin_amdgcn_global_load_lds((const void *)(kt_base + kfo[j]),
-                                             (lds_void *)(Ks + (wave_s * 2 + j) * 512), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[0]), (lds_void *)(Vs + wave_s * 512), 16, 0, 0);
+                                             (lds_void *)(Ks + (wave_s * 4 + j) * 512), 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[j]), (lds_void *)(Vs + (wave_s * 2 + j) * 512), 16, 0, 0);
         if (wave_s == 0)
-            __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[1]), (lds_void *)(Vs + 8 * 512), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[2]), (lds_void *)(Vs + 8 * 512), 16, 0, 0);
     };
     auto zero_tail = [&](int kb, uint16_t *Vs) {   // V^T entries of keys >= k_len -> 0
         const int valid = k_len - kb;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int s = tid + 512 * j;
+        for (int j = 0; j < 3; j++) {
+            const int s = tid + 256 * j;
             if (s < HD * 8) {
                 const int d = s >> 3, c = (s & 7) ^ text::v_swz(d);
                 const int k0 = c * 8;
@@ -116,27 +123,33 @@ __global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
 
     const int n_tiles = (k_len + BK - 1) / BK;
     // V^T rows 72..95 of both buffers stay zero
-    for (int i = tid; i < 2 * (HDV - HD) * BK / 8; i += 512) {
+    for (int i = tid; i < 2 * (HDV - HD) * BK / 8; i += 256) {
         const int b = i / ((HDV - HD) * BK / 8), r = i % ((HDV - HD) * BK / 8);
         *(u32x4 *)((b ? v1s : v0s) + HD * BK + r * 8) = u32x4{0, 0, 0, 0};
     }
     if (n_tiles > 0) load_tiles(0, k0s, v0s);
 
-    // ---- Q: lane holds Q[my_q][32c + 8g + j] (zero past dim 72), the B operand of chunk c.
-    bf16x8 qf[NC];
-    {
-        const uint16_t *src = p.q_plane + ((size_t)h * p.T + qrow) * HD;
+    // ---- Q: half hh of the wave holds rows 32w + 16hh + q16; lane holds Q[row][32c + 8g + j]
+    // (zero past dim 72), the B operand of chunk c.
+    bf16x8 qf[2][NC];
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const int my_q = wave * ROWS + 16 * hh + q16;
+        const bool q_valid = my_q < nq;
+        const uint16_t *src = p.q_plane + ((size_t)h * p.T + (size_t)q_row0 + (q_valid ? my_q : 0)) * HD;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const int ch = 4 * c + g;
             const u32x4 w = (q_valid && ch < RCH) ? *(const u32x4 *)(src + ch * 8) : u32x4{0, 0, 0, 0};
-            qf[c] = __builtin_bit_cast(bf16x8, w);
+            qf[hh][c] = __builtin_bit_cast(bf16x8, w);
         }
     }
-    f32x4 o[NM];
+    f32x4 o[2][NM];
 #pragma unroll
-    for (int mt = 0; mt < NM; mt++) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
+    for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+        for (int mt = 0; mt < NM; mt++) o[hh][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
     const float sl2 = p.scale_log2;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -152,19 +165,20 @@ __global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
         if (t + 1 < n_tiles) load_tiles(kb + BK, Kn, Vn);
         if (wave_live) {
             constexpr int DEPTH = 6, QK = 4 * NC;
-            f32x4 s[4];
+            f32x4 s[2][4];
             bf16x8 ring[DEPTH];
             static_for<DEPTH>([&](auto I) {
                 constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
                 ring[st] = lds_read16<buf * 2 * KTILE>(ka[kt][c]);
             });
-            static_for<QK>([&](auto I) {
+            static_for<QK>([&](auto I) {   // one K operand, both halves' products
                 constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
                 constexpr int ahead = (QK - 1 - st) < (DEPTH - 1) ? (QK - 1 - st) : (DEPTH - 1);
                 bf16x8 a = ring[st % DEPTH];
                 lds_wait<ahead>(a);
-                if constexpr (c == 0) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[kt], 0, 0, 0);
+                if constexpr (c == 0) s[0][kt] = s[1][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                s[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][c], s[0][kt], 0, 0, 0);
+                s[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][c], s[1][kt], 0, 0, 0);
                 if constexpr (st + DEPTH < QK) {
                     constexpr int n = st + DEPTH, nkt = n & 3, nc = n >> 2;
                     ring[st % DEPTH] = lds_read16<buf * 2 * KTILE>(ka[nkt][nc]);
@@ -178,56 +192,64 @@ __global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
             };
             bf16x8 vring[DEPTH];
             static_for<DEPTH>([&](auto I) { vring[decltype(I)::value] = vread(I); });
-            if (kb + BK > k_len) {
-                // element (kt, i) is key kb + 32(kt>>1) + 8g + 4(kt&1) + i
-                const int lim = k_len - 1 - kb - 8 * g;
+            bf16x8 pk[2][2];
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                if (kb + BK > k_len) {
+                    // element (kt, i) is key kb + 32(kt>>1) + 8g + 4(kt&1) + i
+                    const int lim = k_len - 1 - kb - 8 * g;
+#pragma unroll
+                    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            s[hh][kt][i] = (32 * (kt >> 1) + 4 * (kt & 1) + i > lim) ? -INFINITY : s[hh][kt][i];
+                }
+                float mx = -INFINITY;
 #pragma unroll
                 for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        s[kt][i] = (32 * (kt >> 1) + 4 * (kt & 1) + i > lim) ? -INFINITY : s[kt][i];
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kt][i]);
-            mx = xrow_max(mx) * sl2;
-            // The running max moves only when a tile's max passes it by more than 8 (log2 units):
-            // P stays below 2^8, and the O rescale below runs on few tiles.
-            const float mn = (mx > m_run + 8.f) ? mx : m_run;
-            const float msub = (mn == -INFINITY) ? 0.f : mn;
-            const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
-            float rs = 0.f;
-            bf16x8 pk[2];
-#pragma unroll
-            for (int kc = 0; kc < 2; kc++) {
-                unsigned w[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int kt = 2 * kc + (j >> 1), i = 2 * (j & 1);
-                    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][i], sl2, -msub));
-                    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][i + 1], sl2, -msub));
-                    w[j] = pack_bf16(p0, p1);
-                    rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]),
-                                                         bf16x2{(__bf16)1.0f, (__bf16)1.0f}, rs, false);
+                    for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[hh][kt][i]);
+                // The running max moves only when a tile's max passes it by more than 8 (log2
+                // units): P stays below 2^8, and the O rescale below runs on few tiles. The
+                // lane's own max decides whether any row may move; only then is the row max
+                // reduced over the row's four lanes.
+                float mn = m_run[hh];
+                if (__any(mx * sl2 > m_run[hh] + 8.f)) {
+                    const float rmx = xrow_max(mx) * sl2;
+                    mn = (rmx > m_run[hh] + 8.f) ? rmx : m_run[hh];
                 }
-                u32x4 wv = {w[0], w[1], w[2], w[3]};
-                pk[kc] = __builtin_bit_cast(bf16x8, wv);
-            }
-            rs = xrow_sum(rs);
-            l_run = l_run * alpha + rs;
-            m_run = mn;
-            if (__any(alpha != 1.f)) {
+                const float msub = (mn == -INFINITY) ? 0.f : mn;
+                const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run[hh] - mn);
+                float rs = 0.f;
 #pragma unroll
-                for (int mt = 0; mt < NM; mt++) o[mt] *= alpha;
+                for (int kc = 0; kc < 2; kc++) {
+                    unsigned w[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int kt = 2 * kc + (j >> 1), i = 2 * (j & 1);
+                        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[hh][kt][i], sl2, -msub));
+                        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[hh][kt][i + 1], sl2, -msub));
+                        w[j] = pack_bf16(p0, p1);
+                        rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]),
+                                                             bf16x2{(__bf16)1.0f, (__bf16)1.0f}, rs, false);
+                    }
+                    u32x4 wv = {w[0], w[1], w[2], w[3]};
+                    pk[hh][kc] = __builtin_bit_cast(bf16x8, wv);
+                }
+                l_run[hh] = l_run[hh] * alpha + rs;   // the lane's share, rows added up at the end
+                m_run[hh] = mn;
+                if (__any(alpha != 1.f)) {
+#pragma unroll
+                    for (int mt = 0; mt < NM; mt++) o[hh][mt] *= alpha;
+                }
             }
-            static_for<PV>([&](auto I) {
+            static_for<PV>([&](auto I) {   // one V^T operand, both halves' products
                 constexpr int st = decltype(I)::value, mt = st % NM, kc = st / NM;
                 constexpr int ahead = (PV - 1 - st) < (DEPTH - 1) ? (PV - 1 - st) : (DEPTH - 1);
                 bf16x8 a = vring[st % DEPTH];
                 lds_wait<ahead>(a);
-                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[kc], o[mt], 0, 0, 0);
+                o[0][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[0][kc], o[0][mt], 0, 0, 0);
+                o[1][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[1][kc], o[1][mt], 0, 0, 0);
                 if constexpr (st + DEPTH < PV) vring[st % DEPTH] = vread(std::integral_constant<int, st + DEPTH>{});
             });
         }
@@ -240,10 +262,14 @@ __global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
     }
 
     // ---- Epilogue: O / l; lane (q16, g) holds dims 32u + 8g + [0, 8) (stored below dim 72)
-    if (q_valid) {
-        const float il = l_run > 0.f ? 1.f / l_run : 0.f;
+    int32_t *flag = p.ovf ? p.ovf + flag_row : nullptr;
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const int my_q = wave * ROWS + 16 * hh + q16;
+        const float l_row = xrow_sum(l_run[hh]);   // before the row-divergent exit: lanes exchange values
+        if (my_q >= nq) continue;
+        const float il = l_row > 0.f ? 1.f / l_row : 0.f;
         const size_t t = (size_t)q_row0 + my_q;
-        int32_t *flag = p.ovf ? p.ovf + flag_row : nullptr;
 #pragma unroll
         for (int u = 0; u < NC; u++) {
             const int d0 = 32 * u + 8 * g;
@@ -251,8 +277,8 @@ __global__ __launch_bounds__(512, 1) void attn_vis_kernel(AttnParams p) {
             float v[8];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                v[i] = o[2 * u][i] * il;
-                v[4 + i] = o[2 * u + 1][i] * il;
+                v[i] = o[hh][2 * u][i] * il;
+                v[4 + i] = o[hh][2 * u + 1][i] * il;
             }
             store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);
         }
