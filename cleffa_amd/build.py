@@ -6,7 +6,7 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 REPO = ROOT.parent
 LIB = ROOT / "libclef_hip_attn.so"
-SOURCES = [ROOT / "csrc" / "attn_api.hip"]
+SOURCES = [ROOT / "csrc" / "attn_api.hip", ROOT / "csrc" / "records.cpp"]
 DEPS = SOURCES + [ROOT / "csrc" / "attn_kernels.h", ROOT / "csrc" / "attn_params.h",
                   REPO / "include" / "clef_hip_attn.h"]
 

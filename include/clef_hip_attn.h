@@ -151,6 +151,24 @@ typedef struct {
 
 bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen);
 
+/* Host-only producers of the path's inputs. */
+
+/* M-RoPE positions pos3 [T][3] of one record (clef_record.c:938-962, clef_record_positions):
+ * text tokens take (p, p, p) with p counting up from 0; vision span i (an image, or one frame of
+ * a video) starts at token span_start[i] and covers its merged grid, (span_grid_h[i] / merge) x
+ * (span_grid_w[i] / merge) tokens row-major, token (y, x) taking (p, p + y, p + x), after which
+ * p advances by the larger merged side. Spans in token order, not overlapping. */
+bool clef_hip_record_positions(int T, const int32_t *span_start, const int32_t *span_grid_h,
+                               const int32_t *span_grid_w, int n_spans, int merge, int32_t *pos3,
+                               char *err, size_t errlen);
+
+/* Micro-batch packing of the server's queue (clef_server.c:311-327): first in, first out; the
+ * head is always taken, then requests while fewer than max_batch are taken and the tokens stay
+ * within max_tokens; a request with a prefix-cache key (keyed[i] != 0, keyed may be NULL) runs
+ * alone. Writes cu_seqlens[0 .. n] of the n records taken and returns n (0 for an empty queue). */
+int clef_hip_pack_batch(const int32_t *lengths, const uint8_t *keyed, int n_queue, int max_batch,
+                        long max_tokens, int32_t *cu_seqlens);
+
 #ifdef __cplusplus
 }
 #endif
