@@ -48,7 +48,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3", "C4"])
+    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3", "C4", "P"],
+                    help="C1-C4: attention configurations; P: prefix-cache growth copy (HBM-bound)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
@@ -158,6 +159,40 @@ def cpu_baseline(w, cfg):
     return statistics.median(times), oracle.num_threads()
 
 
+def bench_prefix_growth(a):
+    """Growth copy of one layer's prefix-cache planes (nkv 4, hd 256): an entry of 65,536 rows
+    grows to 81,920, keeping all 65,536 (600 MB moved, more than the 256 MB last-level cache).
+    Algorithmic bytes: the kept rows read once, every row of the new planes written once."""
+    import ctypes
+    from cleffa_amd import _lib
+    nkv, hd, src_cap, dst_cap, keep = 4, 256, 65536, 81920, 65536
+    lib = _lib.load()
+    ks = torch.randn(nkv, src_cap, hd, device="cuda").bfloat16()
+    vs = torch.randn(nkv, hd, src_cap, device="cuda").bfloat16()
+    kd = torch.empty(nkv, dst_cap, hd, device="cuda", dtype=torch.bfloat16)
+    vd = torch.empty(nkv, hd, dst_cap, device="cuda", dtype=torch.bfloat16)
+    err = ctypes.create_string_buffer(256)
+
+    def step():
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(lib.clef_hip_prefix_copy(ks.data_ptr(), vs.data_ptr(), src_cap, kd.data_ptr(), vd.data_ptr(),
+                                            dst_cap, nkv, hd, keep, s, err, 256), err)
+
+    ms, wall_ms = time_fn(step, a.steps, a.warmup, not a.no_graph)
+    nbytes = 2 * nkv * hd * 2 * (keep + dst_cap)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "prefix-cache growth copy GB/s (one layer, 4 x 256 planes, 65,536 -> 81,920 rows)",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 5), "host_ms_per_step": round(wall_ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u16", "data": "synthetic",
+        "config": {"workload": "P prefix growth copy", "bytes": nbytes},
+        "roofline": {"bound": "hbm", "kernel": "prefix_copy_kernel", "achieved": round(gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": None, "launch_ms": round(ms, 5)},
+    }), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -168,6 +203,8 @@ def main():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(2)
     torch.cuda.set_device(0)
+    if a.config == "P":
+        return bench_prefix_growth(a)
     step, core, info, w = build_step(a.config, a.seed)
     if a.profile_pass:
         src = torch.randn(CALIB_BYTES // 2, device="cuda").to(torch.bfloat16)

@@ -21,6 +21,7 @@ EXPORTS = (
     "clef_hip_rope_inv_freq", "clef_hip_vis_positions", "clef_hip_attn_prep_kv",
     "clef_hip_attn_core", "clef_hip_attn_prefill", "clef_hip_vis_attention",
     "clef_hip_record_positions", "clef_hip_pack_batch",
+    "clef_hip_prefix_capacity", "clef_hip_prefix_plane_bytes", "clef_hip_prefix_copy",
 )
 
 
@@ -70,6 +71,13 @@ def load():
     lib.clef_hip_record_positions.restype = c_bool
     lib.clef_hip_pack_batch.argtypes = [POINTER(c_int32), ctypes.c_void_p, c_int, c_int, ctypes.c_long, POINTER(c_int32)]
     lib.clef_hip_pack_batch.restype = c_int
+    lib.clef_hip_prefix_capacity.argtypes = [c_int, c_int, c_int]
+    lib.clef_hip_prefix_capacity.restype = c_int
+    lib.clef_hip_prefix_plane_bytes.argtypes = [c_int, c_int, c_int]
+    lib.clef_hip_prefix_plane_bytes.restype = c_size_t
+    lib.clef_hip_prefix_copy.argtypes = [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
+                                         c_void_p, c_char_p, c_size_t]
+    lib.clef_hip_prefix_copy.restype = c_bool
     lib.clef_hip_attn_plan_max_blocks.argtypes = [c_int, c_int]
     lib.clef_hip_attn_plan_max_blocks.restype = c_int
     lib.clef_hip_attn_plan.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int, c_int,

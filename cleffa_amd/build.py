@@ -6,8 +6,9 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 REPO = ROOT.parent
 LIB = ROOT / "libclef_hip_attn.so"
-SOURCES = [ROOT / "csrc" / "attn_api.hip", ROOT / "csrc" / "records.cpp"]
-DEPS = SOURCES + [ROOT / "csrc" / "attn_kernels.h", ROOT / "csrc" / "attn_params.h",
+SOURCES = [ROOT / "csrc" / "attn_api.hip", ROOT / "csrc" / "prefix_cache.hip", ROOT / "csrc" / "records.cpp"]
+DEPS = SOURCES + [ROOT / "csrc" / "attn_kernels.h", ROOT / "csrc" / "attn_params.h", ROOT / "csrc" / "attn_text.h",
+                  ROOT / "csrc" / "attn_vis.h",
                   REPO / "include" / "clef_hip_attn.h"]
 
 

@@ -151,6 +151,28 @@ typedef struct {
 
 bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen);
 
+/* Prefix-cache entry planes (clef_metal.m:15-29 struct clef_gpu_prefix, 762-805 prefix_reserve).
+ * An entry holds, per attention layer, a K plane [nkv][cap][hd] and a V^T plane [nkv][hd][cap],
+ * bf16, rows (columns of V^T) indexed by the record's own token index; a prefix pass uses them as
+ * k_plane / vt_plane with kvT = cap and cu_seqlens_k = {0, L + n}. The caller allocates them.
+ *
+ * clef_hip_prefix_capacity: the capacity an entry of cur_cap rows needs to hold `rows` tokens:
+ * cur_cap when it already fits, else max(rows, cur_cap + cur_cap / 4) rounded up to a multiple of
+ * 1024 (an entry that keeps growing is copied a handful of times, not every 1,024 tokens).
+ * Returns -1 when the planes would pass the 32-bit plane offsets of the kernels (cap * hd * 2 >=
+ * 2^32) or `rows` is negative. */
+int clef_hip_prefix_capacity(int rows, int cur_cap, int hd);
+/* Bytes of one plane (K or V^T) of one layer: nkv * cap * hd * 2. */
+size_t clef_hip_prefix_plane_bytes(int nkv, int hd, int cap);
+/* Growth copy of one layer's planes (the memcpy loop of prefix_reserve): dst rows [0, keep) take
+ * the src rows, dst rows [keep, dst_cap) are zeroed (Metal's zero-filled new buffers). K planes
+ * copy whole rows; V^T planes copy the first `keep` columns of each of the nkv * hd rows. One
+ * kernel on `stream` covers both planes. src_cap and dst_cap multiples of 8, keep <= both,
+ * pointers 16-byte aligned, src and dst not overlapping. */
+bool clef_hip_prefix_copy(const uint16_t *k_src, const uint16_t *vt_src, int src_cap,
+                          uint16_t *k_dst, uint16_t *vt_dst, int dst_cap, int nkv, int hd, int keep,
+                          void *stream, char *err, size_t errlen);
+
 /* Host-only producers of the path's inputs. */
 
 /* M-RoPE positions pos3 [T][3] of one record (clef_record.c:938-962, clef_record_positions):
