@@ -48,8 +48,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3", "C4", "P"],
-                    help="C1-C4: attention configurations; P: prefix-cache growth copy (HBM-bound)")
+    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3", "C4", "P", "O"],
+                    help="C1-C4: attention configurations; P: prefix-cache growth copy (HBM-bound); "
+                         "O: Omni attention (hd 128, FP32, 16,344 tokens)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
@@ -193,6 +194,50 @@ def bench_prefix_growth(a):
     }), flush=True)
 
 
+PEAK_F32_MFMA = 157.3       # MI355X dense fp32 MFMA TFLOP/s (published)
+PEAK_F64_MFMA = 78.6        # MI355X dense fp64 MFMA TFLOP/s (published)
+
+
+def bench_omni(a):
+    """Omni decoder attention, one causal record of 16,344 tokens (the largest default length of
+    bench/omni_attention_bench.m), 32/4 heads, hd 128, FP32 operands. Step = prep + attention.
+    Half the flops (S = Q.K^T) run on fp32 MFMA and half (P.V) on fp64 MFMA, so the matrix-core
+    ceiling for the attention kernel is 2 / (1/157.3 + 1/78.6) = 104.8 TFLOP/s."""
+    from cleffa_amd.omni import OmniAttention, OmniPlan
+    T, nh, nkv = 16344, 32, 4
+    g = torch.Generator(device="cuda")
+    g.manual_seed(a.seed)
+    qkv = torch.randn(T, (nh + 2 * nkv) * 128, generator=g, device="cuda")
+    qn = 1 + 0.1 * torch.randn(128, generator=g, device="cuda")
+    kn = 1 + 0.1 * torch.randn(128, generator=g, device="cuda")
+    pos3 = torch.arange(T, device="cuda", dtype=torch.int32)[:, None].repeat(1, 3).contiguous()
+    att = OmniAttention(nh, nkv)
+    plan = OmniPlan([0, T])
+    planes = att.planes(T)
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = torch.empty(T, nh * 128, device="cuda")
+    step = lambda: (att.prep(qkv, qn, kn, pos3, planes=planes, status=status), att.attention(*planes, plan, out=out))
+    core = lambda: att.attention(*planes, plan, out=out)
+    step()
+    ms, wall_ms = time_fn(step, a.steps, a.warmup, not a.no_graph)
+    core_ms, _ = time_fn(core, a.steps, a.warmup, not a.no_graph)
+    flops = 4.0 * 128 * nh * plan.pairs()
+    peak = 2.0 / (1.0 / PEAK_F32_MFMA + 1.0 / PEAK_F64_MFMA)
+    achieved = flops / (core_ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "Omni attention TFLOP/s (16,344-token causal record, 32/4 heads, hd 128, FP32 in, FP64 accumulate)",
+        "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+        "tokens_per_s": round(T / (ms * 1e-3), 1), "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 5), "host_ms_per_step": round(wall_ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded N(0,1))",
+        "config": {"workload": "O Omni attention: 1 x 16,344 tokens, 32/4 heads, hd 128", "gflop": round(flops / 1e9, 2)},
+        "roofline": {"bound": "mfma", "kernel": "omni_attn_kernel<8>", "achieved": round(achieved, 2),
+                     "peak": round(peak, 1), "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
+                     "traffic": None, "launch_ms": round(core_ms, 5)},
+        "prep_ms": round(ms - core_ms, 5),
+    }), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -205,6 +250,8 @@ def main():
     torch.cuda.set_device(0)
     if a.config == "P":
         return bench_prefix_growth(a)
+    if a.config == "O":
+        return bench_omni(a)
     step, core, info, w = build_step(a.config, a.seed)
     if a.profile_pass:
         src = torch.randn(CALIB_BYTES // 2, device="cuda").to(torch.bfloat16)

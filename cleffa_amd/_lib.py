@@ -21,6 +21,8 @@ EXPORTS = (
     "clef_hip_rope_inv_freq", "clef_hip_vis_positions", "clef_hip_attn_prep_kv",
     "clef_hip_attn_core", "clef_hip_attn_prefill", "clef_hip_vis_attention",
     "clef_hip_record_positions", "clef_hip_pack_batch",
+    "clef_hip_omni_rope_table", "clef_hip_omni_prep", "clef_hip_omni_plan_max_blocks",
+    "clef_hip_omni_plan", "clef_hip_omni_attention",
     "clef_hip_prefix_capacity", "clef_hip_prefix_plane_bytes", "clef_hip_prefix_copy",
 )
 
@@ -50,6 +52,22 @@ class VisArgs(ctypes.Structure):
     ]
 
 
+class OmniPrepArgs(ctypes.Structure):
+    _fields_ = [
+        ("nh", c_int), ("nkv", c_int), ("T", c_int), ("kvT", c_int), ("eps", c_float), ("rope_exact", c_int),
+        ("qkv", c_void_p), ("q_norm", c_void_p), ("k_norm", c_void_p), ("pos3", c_void_p), ("freq", c_void_p),
+        ("q_plane", c_void_p), ("k_plane", c_void_p), ("v_plane", c_void_p), ("status", c_void_p),
+    ]
+
+
+class OmniAttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("nh", c_int), ("nkv", c_int), ("T", c_int), ("kvT", c_int), ("scale", c_float),
+        ("q_plane", c_void_p), ("k_plane", c_void_p), ("v_plane", c_void_p), ("blocks", c_void_p),
+        ("n_blk", c_int), ("out", c_void_p),
+    ]
+
+
 _lib = None
 
 
@@ -71,6 +89,17 @@ def load():
     lib.clef_hip_record_positions.restype = c_bool
     lib.clef_hip_pack_batch.argtypes = [POINTER(c_int32), ctypes.c_void_p, c_int, c_int, ctypes.c_long, POINTER(c_int32)]
     lib.clef_hip_pack_batch.restype = c_int
+    lib.clef_hip_omni_rope_table.argtypes = [c_float, POINTER(c_float)]
+    lib.clef_hip_omni_rope_table.restype = None
+    lib.clef_hip_omni_prep.argtypes = [POINTER(OmniPrepArgs), c_void_p, c_char_p, c_size_t]
+    lib.clef_hip_omni_prep.restype = c_bool
+    lib.clef_hip_omni_plan_max_blocks.argtypes = [c_int, c_int]
+    lib.clef_hip_omni_plan_max_blocks.restype = c_int
+    lib.clef_hip_omni_plan.argtypes = [POINTER(c_int32), c_int, POINTER(c_int32), c_int, POINTER(c_int),
+                                       c_char_p, c_size_t]
+    lib.clef_hip_omni_plan.restype = c_bool
+    lib.clef_hip_omni_attention.argtypes = [POINTER(OmniAttnArgs), c_void_p, c_char_p, c_size_t]
+    lib.clef_hip_omni_attention.restype = c_bool
     lib.clef_hip_prefix_capacity.argtypes = [c_int, c_int, c_int]
     lib.clef_hip_prefix_capacity.restype = c_int
     lib.clef_hip_prefix_plane_bytes.argtypes = [c_int, c_int, c_int]

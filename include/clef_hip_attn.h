@@ -151,6 +151,56 @@ typedef struct {
 
 bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen);
 
+/* ---- Omni decoder attention (metal/clef.metal:2055-2319 omni_attn_prep / omni_attention, host
+ * clef_metal_omni.m:200-245 clef_omni_encode_attention). FP32 operands, hd 128, causal within
+ * each record, no gate; the output is accumulated in FP64 (the reference: FP32 hi/lo pairs).
+ *
+ * clef_hip_omni_rope_table: the 192-float rotary table of the reference (clef_metal.m:172-180):
+ * [0, 64) 1 / theta^(2j/128) in FP32, [64, 128) and [128, 192) the FP64 theta^(-2j/128) as an
+ * FP32 hi / lo pair. */
+#define CLEF_HIP_OMNI_BLOCK_Q 16   /* query rows per block */
+#define CLEF_HIP_OMNI_SLACK 32     /* zero rows after each kv head's T rows (kvT >= T + 32) */
+void clef_hip_omni_rope_table(float theta, float *freq192);
+
+/* omni_attn_prep: per pass row t and head h, RMSNorm (weights as given) and rotary over all 128
+ * dims (pairs (i, i + 64), pair i turning by pos3 axis i % 3 for i < 60 and axis 0 above),
+ * with the angle from the FP64 frequency reduced in FP64 (rope_exact) or the FP32 product
+ * pos * freq[i] (rope_exact 0, CLEF_OMNI_ROPE=f32). Writes Q [nh][T][128], K and V [nkv][kvT][128]
+ * (V copied), zeroes K / V rows T .. T+31, and ORs 2 into *status when any input or output value
+ * is not finite. */
+typedef struct {
+    int nh, nkv, T, kvT;
+    float eps;
+    int rope_exact;
+    const float *qkv;         /* [T][(nh + 2 nkv) * 128]: Q heads, K heads, V heads */
+    const float *q_norm, *k_norm;   /* [128] */
+    const int32_t *pos3;      /* [T][3] */
+    const float *freq;        /* [192], clef_hip_omni_rope_table */
+    float *q_plane, *k_plane, *v_plane;
+    uint32_t *status;
+} clef_hip_omni_prep_args;
+bool clef_hip_omni_prep(const clef_hip_omni_prep_args *a, void *stream, char *err, size_t errlen);
+
+/* Block list of an Omni pass: 16-row query blocks per record, each with its record's keys from
+ * the record's first row (seq_start of the reference), longest first. Entries as for
+ * clef_hip_attn_plan: {q_row0, nq, q_pos0, k_row0, k_len, 0, record, 0}. */
+int clef_hip_omni_plan_max_blocks(int n_seq, int T);
+bool clef_hip_omni_plan(const int32_t *cu_seqlens, int n_seq, int32_t *blocks, int max_blocks, int *n_blk,
+                        char *err, size_t errlen);
+
+/* omni_attention: out[t][h*128 + d] = sum_s softmax(scale * Q_h[t] . K_kh[s]) V_kh[s][d] over the
+ * keys s <= t of t's record, FP32 output. Key tiles start at each record's first row, so a
+ * record's output bytes do not depend on what else is packed with it. */
+typedef struct {
+    int nh, nkv, T, kvT;
+    float scale;
+    const float *q_plane, *k_plane, *v_plane;
+    const int32_t *blocks;
+    int n_blk;
+    float *out;               /* [T][nh * 128] */
+} clef_hip_omni_attn_args;
+bool clef_hip_omni_attention(const clef_hip_omni_attn_args *a, void *stream, char *err, size_t errlen);
+
 /* Prefix-cache entry planes (clef_metal.m:15-29 struct clef_gpu_prefix, 762-805 prefix_reserve).
  * An entry holds, per attention layer, a K plane [nkv][cap][hd] and a V^T plane [nkv][hd][cap],
  * bf16, rows (columns of V^T) indexed by the record's own token index; a prefix pass uses them as

@@ -20,6 +20,11 @@
  *                     ref/safe_attn.py:25-52 and 55-68 (semantics), metal/clef.metal:316-352
  *                     (reference kernel, gate epilogue), 709-849 (prefix mask key <= q + qoff),
  *                     930-1093 (block list qbase/kbase addressing).
+ *   orc_omni_prep_*   omni_attn_prep: hd-128 RMSNorm (weights as given) and full rotary over 64
+ *                     pairs, axis i % 3 below pair 60 and axis 0 above, angle from the FP64
+ *                     frequency (exact) or the f32 product; metal/clef.metal:2055-2131, checked
+ *                     the way tests/test_omni_attention.m:104-122 checks it. Omni attention
+ *                     itself is orc_attention_* with no gate (metal/clef.metal:2165-2319).
  *   orc_vis_prep_*    vis_qkv_rope: bias add, 2-D rotary on pairs (i, i + hd/2), first hd/4 pairs
  *                     by grid row, the rest by grid column; metal/clef.metal:1616-1656.
  */

@@ -129,3 +129,40 @@ void SFX(orc_vis_prep)(int P, int heads, int hd, const float *qkv, const float *
         }
     }
 }
+
+/* metal/clef.metal:2074-2131 (omni_attn_prep) as tests/test_omni_attention.m:104-122 checks it:
+ * qkv [T][(nh + 2 nkv) * 128] f32 holds [nh Q] [nkv K] [nkv V]; per head RMSNorm with the weights
+ * as given, then rotary over all 64 pairs (i, i + 64), pair i by pos3 axis i % 3 for i < 60 and
+ * axis 0 for the last four. exact != 0: angle = pos * theta^(-2i/128) in REAL; exact == 0: the
+ * f32 product (float)pos * inv_freq[i]. Q [nh][T][128], K / V [nkv][T][128]. */
+void SFX(orc_omni_prep)(int T, int nh, int nkv, double eps, int exact, double theta,
+                        const float *qkv, const float *qnorm, const float *knorm,
+                        const int32_t *pos3, const float *inv_freq, REAL *Q, REAL *K, REAL *V) {
+    const int hd = 128, row = (nh + 2 * nkv) * hd;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int t = 0; t < T; t++) {
+        for (int head = 0; head < nh + nkv; head++) {
+            const float *src = qkv + (size_t)t * row + (size_t)head * hd;
+            const int is_q = head < nh, kh = head - nh;
+            const float *w = is_q ? qnorm : knorm;
+            REAL *dst = is_q ? Q + ((size_t)head * T + t) * hd : K + ((size_t)kh * T + t) * hd;
+            REAL ss = 0;
+            for (int d = 0; d < hd; d++) ss += (REAL)src[d] * (REAL)src[d];
+            const REAL inv = (REAL)1 / sqrt(ss / (REAL)hd + (REAL)eps);
+            for (int d = 0; d < hd; d++) dst[d] = (REAL)src[d] * inv * (REAL)w[d];
+            for (int i = 0; i < 64; i++) {
+                const int position = pos3[3 * (size_t)t + (i < 60 ? i % 3 : 0)];
+                const REAL ang = exact ? (REAL)((double)position * pow(theta, -2.0 * i / 128.0))
+                                       : (REAL)((float)position * inv_freq[i]);
+                const REAL c = cos(ang), s = sin(ang);
+                const REAL x0 = dst[i], x1 = dst[i + 64];
+                dst[i] = x0 * c - x1 * s;
+                dst[i + 64] = x1 * c + x0 * s;
+            }
+            if (!is_q) {
+                const float *vs = qkv + (size_t)t * row + (size_t)(nh + nkv + kh) * hd;
+                for (int d = 0; d < hd; d++) V[((size_t)kh * T + t) * hd + d] = (REAL)vs[d];
+            }
+        }
+    }
+}

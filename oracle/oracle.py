@@ -38,6 +38,9 @@ def load():
             fn = getattr(lib, f"orc_vis_prep_{sfx}")
             fn.argtypes = [c_int, c_int, c_int] + [c_void_p] * 7
             fn.restype = None
+            fn = getattr(lib, f"orc_omni_prep_{sfx}")
+            fn.argtypes = [c_int, c_int, c_int, c_double, c_int, c_double] + [c_void_p] * 8
+            fn.restype = None
         lib.orc_num_threads.restype = c_int
         _lib = lib
     return _lib
@@ -109,4 +112,20 @@ def vis_prep(qkv, heads, hd, bias, pos2, inv_freq, precision="f64"):
     Q = np.empty((heads, P, hd), dt); K = np.empty_like(Q); V = np.empty_like(Q)
     getattr(lib, f"orc_vis_prep_{precision}")(P, heads, hd, _p(qkv), _p(_f32(bias)), _p(_i32(pos2)),
                                               _p(_f32(inv_freq)), _p(Q), _p(K), _p(V))
+    return Q, K, V
+
+
+def omni_prep(qkv, nh, nkv, q_norm, k_norm, pos3, theta=1e6, exact=True, inv_freq=None, eps=1e-6,
+              precision="f64"):
+    """Q [nh][T][128], K, V [nkv][T][128] of Omni's attention prep (metal/clef.metal:2074-2131).
+    exact=False needs inv_freq [64] (the f32 table): angle = (float)pos * inv_freq[i]."""
+    lib = load()
+    dt = _dt(precision)
+    qkv = _f32(qkv)
+    T = qkv.shape[0]
+    Q = np.empty((nh, T, 128), dt); K = np.empty((nkv, T, 128), dt); V = np.empty_like(K)
+    inv = _f32(inv_freq) if inv_freq is not None else np.zeros(64, np.float32)
+    getattr(lib, f"orc_omni_prep_{precision}")(T, nh, nkv, eps, int(bool(exact)), float(theta), _p(qkv),
+                                               _p(_f32(q_norm)), _p(_f32(k_norm)), _p(_i32(pos3)), _p(inv),
+                                               _p(Q), _p(K), _p(V))
     return Q, K, V
