@@ -48,9 +48,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3", "C4", "P", "O"],
+    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3", "C4", "P", "O", "G"],
                     help="C1-C4: attention configurations; P: prefix-cache growth copy (HBM-bound); "
-                         "O: Omni attention (hd 128, FP32, 16,344 tokens)")
+                         "O: Omni attention (hd 128, FP32, 16,344 tokens); G: the QKV and o_proj GEMMs around C1")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
@@ -238,6 +238,44 @@ def bench_omni(a):
     }), flush=True)
 
 
+def bench_gemms(a):
+    """The projections either side of the C1 layer at the 27B model's widths (H 5120, 24 x 256
+    query + gate, 4 x 256 K and V): QKV [4096 x 5120] . [14336 x 5120]^T -> bf16 qkv rows, and
+    o_proj [4096 x 6144] . [5120 x 6144]^T accumulated into the f32 residual. Step = both."""
+    from cleffa_amd.gemm import gemm
+    T, H, nq = 4096, 5120, 6144
+    nqkv = 2 * nq + 2 * 4 * 256
+    g = torch.Generator(device="cuda")
+    g.manual_seed(a.seed)
+    xn = torch.randn(T, H, generator=g, device="cuda").bfloat16()
+    wqkv = (0.02 * torch.randn(nqkv, H, generator=g, device="cuda")).bfloat16()
+    attn = torch.randn(T, nq, generator=g, device="cuda").bfloat16()
+    wo = (0.02 * torch.randn(H, nq, generator=g, device="cuda")).bfloat16()
+    qkv = torch.empty(T, nqkv, dtype=torch.bfloat16, device="cuda")
+    resid = torch.zeros(T, H, device="cuda")
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    f_qkv, f_o = 2.0 * T * nqkv * H, 2.0 * T * H * nq
+    qkv_fn = lambda: gemm(xn, wqkv, Y=qkv, out="bf16", workspace=ws)
+    o_fn = lambda: gemm(attn, wo, Y=resid, out="f32", acc=True, workspace=ws)
+    qkv_fn(); o_fn()
+    ms_q, _ = time_fn(qkv_fn, a.steps, a.warmup, not a.no_graph)
+    ms_o, _ = time_fn(o_fn, a.steps, a.warmup, not a.no_graph)
+    tq, to = f_qkv / (ms_q * 1e-3) / 1e12, f_o / (ms_o * 1e-3) / 1e12
+    ms = ms_q + ms_o
+    print(json.dumps({
+        "metric": "QKV + o_proj GEMM TFLOP/s (C1 layer, 4,096 tokens, 27B widths)",
+        "value": round((f_qkv + f_o) / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1))",
+        "config": {"workload": "G: QKV 4096x14336x5120 -> bf16, o_proj 4096x5120x6144 += f32"},
+        "qkv": {"ms": round(ms_q, 5), "tflops": round(tq, 1), "frac": round(tq / PEAK_BF16_TFLOPS, 4)},
+        "o_proj": {"ms": round(ms_o, 5), "tflops": round(to, 1), "frac": round(to / PEAK_BF16_TFLOPS, 4)},
+        "roofline": {"bound": "mfma", "kernel": "hipBLASLt (QKV)", "achieved": round(tq, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tq / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "launch_ms": round(ms_q, 5)},
+    }), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -252,6 +290,8 @@ def main():
         return bench_prefix_growth(a)
     if a.config == "O":
         return bench_omni(a)
+    if a.config == "G":
+        return bench_gemms(a)
     step, core, info, w = build_step(a.config, a.seed)
     if a.profile_pass:
         src = torch.randn(CALIB_BYTES // 2, device="cuda").to(torch.bfloat16)

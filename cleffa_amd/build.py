@@ -6,7 +6,8 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 REPO = ROOT.parent
 LIB = ROOT / "libclef_hip_attn.so"
-SOURCES = [ROOT / "csrc" / "attn_api.hip", ROOT / "csrc" / "prefix_cache.hip", ROOT / "csrc" / "omni_api.hip", ROOT / "csrc" / "records.cpp"]
+SOURCES = [ROOT / "csrc" / "attn_api.hip", ROOT / "csrc" / "prefix_cache.hip", ROOT / "csrc" / "omni_api.hip", ROOT / "csrc" / "records.cpp",
+           ROOT / "csrc" / "gemm_api.cpp"]
 DEPS = SOURCES + [ROOT / "csrc" / "attn_kernels.h", ROOT / "csrc" / "attn_params.h", ROOT / "csrc" / "attn_text.h",
                   ROOT / "csrc" / "attn_vis.h", ROOT / "csrc" / "omni_attn.h",
                   REPO / "include" / "clef_hip_attn.h"]
@@ -18,7 +19,8 @@ def hipcc_command(out=LIB):
             # packed fp32 VALU ops are kept out of the generated code (see DESIGN notes)
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
             "-I", str(REPO / "include"), "-I", str(ROOT / "csrc"),
-            *[str(s) for s in SOURCES], "-o", str(out)]
+            *[str(s) for s in SOURCES], "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib",
+            "-o", str(out)]
 
 
 def build(verbose=False):

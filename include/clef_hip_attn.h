@@ -151,6 +151,18 @@ typedef struct {
 
 bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen);
 
+/* ---- The GEMMs either side of the path (clef_metal.m:463-499 clef_metal_gemm; callers
+ * clef_metal.m:1326 QKV projection, 1415 o_proj into the residual).
+ * Y[T][N] (+)= X[T][K] . W[N][K]^T with X and W bf16 row-major, f32 accumulation. y_type
+ * CLEF_HIP_GEMM_Y_BF16 writes bf16 (the qkv rows clef_hip_attn_prefill reads), CLEF_HIP_GEMM_Y_F32
+ * f32; acc != 0 adds into an f32 Y (the residual stream). workspace (may be NULL with ws_bytes 0)
+ * is device scratch the algorithm may use. Runs on hipBLASLt; the algorithm of each shape is
+ * chosen on its first call. */
+#define CLEF_HIP_GEMM_Y_F32 0
+#define CLEF_HIP_GEMM_Y_BF16 1
+bool clef_hip_gemm(int T, int N, int K, const uint16_t *X, const uint16_t *W, void *Y, int y_type, int acc,
+                   void *workspace, size_t ws_bytes, void *stream, char *err, size_t errlen);
+
 /* ---- Omni decoder attention (metal/clef.metal:2055-2319 omni_attn_prep / omni_attention, host
  * clef_metal_omni.m:200-245 clef_omni_encode_attention). FP32 operands, hd 128, causal within
  * each record, no gate; the output is accumulated in FP64 (the reference: FP32 hi/lo pairs).
