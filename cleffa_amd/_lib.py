@@ -4,10 +4,11 @@ The library is the product: there is no Python or CPU fallback. Loading fails lo
 shared library has not been built.
 """
 import ctypes
+import os
 from ctypes import POINTER, c_bool, c_char_p, c_float, c_int, c_int32, c_size_t, c_uint16, c_void_p
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libclef_hip_attn.so"
+LIB_PATH = Path(os.environ.get("CLEF_HIP_ATTN_LIB") or Path(__file__).resolve().parent / "libclef_hip_attn.so")
 
 OUT_BF16, OUT_F16, OUT_F32 = 0, 1, 2
 BLOCK_Q = 128

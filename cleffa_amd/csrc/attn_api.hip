@@ -76,6 +76,25 @@ bool check_text(const clef_hip_attn_args *a, bool need_core, char *err, size_t e
     return true;
 }
 
+// Grid of the text kernel: one workgroup per CU looping over its items, so that the next item's
+// loads overlap the current one's epilogue (measured 2-3% faster at C1, 1% at C2), or one
+// workgroup per item with CLEF_HIP_TEXT_PERSISTENT=0.
+bool text_persistent() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("CLEF_HIP_TEXT_PERSISTENT");
+        v = (e && e[0] == '0') ? 0 : 1;
+    }
+    return v == 1;
+}
+
+long device_cus() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    return n;
+}
+
 }  // namespace
 
 extern "C" {
@@ -221,9 +240,16 @@ bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, si
     p.causal = a->causal ? 1 : 0; p.gate = a->gate ? 1 : 0; p.out_type = a->out_type;
     p.out_ld = a->nh * a->hd;
     p.trace = a->trace;
+    p.n_blk = a->n_blk;
     p.xcd_heads = (a->nh % 8 == 0 && (a->nh / 8) > 0 && ((a->nh / a->nkv) % (a->nh / 8) == 0 || (a->nh / 8) % (a->nh / a->nkv) == 0)) ? a->nh / 8 : 0;
-    const long grid = (long)a->n_blk * a->nh;
-    if (grid > 0x7fffffffL) return fail(err, errlen, "grid too large");
+    const long n_items = (long)a->n_blk * a->nh;
+    if (n_items > 0x7fffffffL) return fail(err, errlen, "grid too large");
+    long grid = n_items;
+    if (text_persistent()) {
+        // one workgroup per CU, each looping over its items (a multiple of 8 for the XCD mapping)
+        const long cus = device_cus();
+        if (cus > 0 && cus < n_items) grid = p.xcd_heads ? std::max(8L, cus / 8 * 8) : cus;
+    }
     if (a->n_rot == 64)
         hipLaunchKernelGGL(attn_text_kernel<64>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);
     else

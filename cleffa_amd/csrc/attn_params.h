@@ -21,6 +21,7 @@ struct AttnParams {
     int row, T, kvT, nh, nkv, n_rot;
     float eps, scale_log2, f16_lim;
     int causal, gate, out_type, out_ld;
+    int n_blk;                // blocks in the plan (work items = n_blk * nh)
     int xcd_heads;            // nh / 8 when heads split evenly over the 8 XCDs, else 0
     uint64_t *trace;          // NULL, or [grid][8] per-workgroup start, end, HW_ID, XCC_ID, prologue end, loop end
 };

@@ -28,6 +28,7 @@
 namespace clef_hip {
 
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) int i32x8;
 
 namespace text {
 constexpr int HD = 256;                 // head dim
@@ -91,42 +92,60 @@ __device__ __forceinline__ void static_for(F &&f) {
 }
 }  // namespace text
 
-// One (query block, q head) work item.
+// Work items are (query block, q head) pairs. Workgroup b takes items get(0), get(1), ... from a
+// static list. With xcd_heads, the items of XCD x (workgroup ids go round-robin over the 8 XCDs,
+// each with its own L2) are the heads x*xcd_heads .. +xcd_heads-1 of every block, so an XCD
+// streams the K/V of as few kv heads as possible; items keep the plan's longest-first block
+// order and are dealt to the XCD's workgroups in snake order (round r left to right when r is
+// even, right to left when odd), so long and short blocks mix. A grid of one workgroup per item
+// gives every workgroup exactly one.
+struct ItemList {
+    int n_items, per_x, gx, xh, nh;
+    __device__ __forceinline__ void setup(const AttnParams &p) {
+        nh = p.nh;
+        xh = p.xcd_heads;
+        gx = (int)gridDim.x >> 3;
+        n_items = p.n_blk * p.nh;
+        per_x = xh ? p.n_blk * xh : 0;
+    }
+    // the k-th item of this workgroup as block * nh + head, or -1
+    __device__ __forceinline__ int get(int k) const {
+        if (xh && gx && ((int)gridDim.x & 7) == 0) {
+            const int x = blockIdx.x & 7, wl = blockIdx.x >> 3;
+            const int j = k * gx + ((k & 1) ? gx - 1 - wl : wl);
+            if (j >= per_x) return -1;
+            const int bi = j / xh;
+            return bi * nh + x * xh + (j - bi * xh);
+        }
+        const int G = gridDim.x;
+        const int j = k * G + ((k & 1) ? G - 1 - (int)blockIdx.x : (int)blockIdx.x);
+        return j < n_items ? j : -1;
+    }
+};
+
+// A workgroup's loop over its items. While one item's epilogue runs (sigmoid gate, stores), the
+// next item's Q rows and first K / V^T tile load by DMA into the LDS buffers the finished key loop
+// left free, and its rotary cos/sin into registers.
 template <int NROT>
-__device__ __forceinline__ void text_block(const AttnParams &p, const int bi, const int h,
-                                           uint16_t *smem, float *qn_lds, uint64_t *tr) {
+__device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, float *qn_lds, uint64_t *tr) {
     using namespace text;
     static_assert(NROT % 64 == 0 && NROT <= HD, "rotary pairs must sit in one lane");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int q16 = lane & 15, g = lane >> 4;
+    ItemList items;
+    items.setup(p);
+    int item = items.get(0);
+    if (item < 0) return;
 
-    const int32_t *blk = p.blocks + 8 * bi;
-    const int q_row0 = blk[0], nq = blk[1], q_pos0 = blk[2], k_row0 = blk[3], k_len = blk[4];
-    const int flag_row = blk[5];
-    const int kh = h / (p.nh / p.nkv);
-
-    const int my_q = wave * ROWS + q16;
-    const bool q_valid = my_q < nq;
-    const int qpos = q_pos0 + my_q;
-    const bool wave_live = wave * ROWS < nq;
-    const int wave_last_pos = q_pos0 + wave * ROWS + ROWS - 1;
-    const size_t qrow = (size_t)q_row0 + (q_valid ? my_q : 0);
-
-    // ---- tiles
-    const uint16_t *kbase = p.k_plane + ((size_t)kh * p.kvT + k_row0) * HD;
-    const uint16_t *vbase = p.vt_plane + (size_t)kh * HD * p.kvT + k_row0;
-
-    // Wave w fills slots [(4w + j) * 64, +64) of each 2048-slot tile, one global_load_lds per j.
-    // K slot s: key s/32, chunk (s%32) ^ k_swz(key). V^T slot s: dim s/8, chunk (s%8) ^ v_swz(dim).
-    // Rows past the record are clamped to valid addresses; their scores are masked and their
-    // values zeroed in LDS before use.
     // LDS: K0 | K1 | V0 | V1 (32 KB each). Operand reads address K buffers from the LDS base and
     // V buffers from base + 64 KB, so the buffer choice is an immediate offset.
     uint16_t *const k0s = smem, *const k1s = smem + KTILE, *const v0s = smem + 2 * KTILE,
                    *const v1s = smem + 2 * KTILE + VTILE;
-    // Fills use a wave-uniform tile base plus loop-invariant per-lane byte offsets. Tiles may
-    // reach past the record's last key (up to the 64-key boundary): the plan sizes the planes so
-    // that those reads stay inside them, their scores are masked and their V^T entries zeroed.
+    // Wave w fills slots [(4w + j) * 64, +64) of each 2048-slot tile, one global_load_lds per j.
+    // K slot s: key s/32, chunk (s%32) ^ k_swz(key). V^T slot s: dim s/8, chunk (s%8) ^ v_swz(dim).
+    // Tiles may reach past the record's last key (up to the 64-key boundary): the plan sizes the
+    // planes so that those reads stay inside them, their scores are masked and their V^T entries
+    // zeroed in LDS before use.
     const int wave_s = __builtin_amdgcn_readfirstlane(wave);
     unsigned kfo[4], vfo[4];
 #pragma unroll
@@ -137,52 +156,7 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
         const int d = grp * 8 + (lane >> 3);
         vfo[j] = ((unsigned)d * (unsigned)p.kvT + (unsigned)(((lane & 7) ^ v_swz(d)) * 8)) * 2u;
     }
-    auto load_tiles = [&](int kb, uint16_t *Ks, uint16_t *Vs) {
-        const char *kt_base = (const char *)(kbase + (size_t)kb * HD);
-        const char *vt_base = (const char *)(vbase + kb);
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(kt_base + kfo[j]),
-                                             (lds_void *)(Ks + (wave_s * 4 + j) * 512), 16, 0, 0);
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[j]),
-                                             (lds_void *)(Vs + (wave_s * 4 + j) * 512), 16, 0, 0);
-    };
-    // Q or gate rows of the block (128 x 256 bf16 = 64 KB, `off` 0 or HD within the head's
-    // 2*HD columns): rows 0-63 into G0, 64-127 into G1, slot s of a half = row s/32, 16-byte
-    // chunk (s%32) ^ (row & 15).
-    auto load_rows = [&](uint16_t *G0, uint16_t *G1, const int off) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int grp = wave * 8 + j;   // 64-slot group, 0..63
-            const int row = grp * 2 + (lane >> 5);
-            const int c = (lane & 31) ^ (row & 15);
-            int rc = min(row, nq - 1);
-            asm volatile("" : "+v"(rc));   // keeps the address math here, not hoisted out of the tile loop
-            uint16_t *dst = (grp < 32 ? G0 : G1) + (grp & 31) * 512;
-            __builtin_amdgcn_global_load_lds((const void *)(p.qkv + ((size_t)q_row0 + rc) * p.row + (size_t)h * 2 * HD + off + c * 8),
-                                             (lds_void *)dst, 16, 0, 0);
-        }
-    };
-    auto zero_tail = [&](int kb, uint16_t *Vs) {   // V^T entries of keys >= k_len -> 0
-        const int valid = k_len - kb;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int s = tid + 512 * j;
-            const int d = s >> 3, c = (s & 7) ^ v_swz(d);
-            const int k0 = c * 8;
-            u32x4 w = *(u32x4 *)(Vs + s * 8);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const unsigned keep = (k0 + 2 * e + 1 < valid) ? 0xffffffffu : (k0 + 2 * e < valid ? 0xffffu : 0u);
-                w[e] &= keep;
-            }
-            *(u32x4 *)(Vs + s * 8) = w;
-        }
-    };
-
-    // per-lane LDS element offsets of the A operands
+    // per-lane LDS byte addresses of the A operands
     const unsigned kl = lds_addr(smem), vl = kl + 2 * 2 * KTILE;
     unsigned ka[4][4];   // byte address of (S tile kt, chunk c & 3) in K0; c >> 2 and K1 are offsets
 #pragma unroll
@@ -196,290 +170,400 @@ __device__ __forceinline__ void text_block(const AttnParams &p, const int bi, co
     const int vx = v_swz(vrow);                      // the mt part does not change the swizzle
     const unsigned va0 = vl + 2 * (vrow * BK + ((g ^ vx) * 8));
     const unsigned va1 = vl + 2 * (vrow * BK + (((4 + g) ^ vx) * 8));
+    const unsigned qn_addr = lds_addr((const uint16_t *)qn_lds);
+    constexpr int R = NROT / 64;
 
-    const int n_tiles = (k_len + BK - 1) / BK;
-    // ---- Q prologue: lane holds Q[my_q][c*32 + 8g + j], the B operand of chunk c.
-    // Every prologue load is issued before any of them is waited for: q_norm (one element per
-    // thread, staged in LDS), the row's rotary cos/sin, the Q row chunks, then the first tile.
-    bf16x8 qf[NC];
-    {
-        const float qn_v = (p.q_norm && tid < HD) ? p.q_norm[tid] : 0.f;
-        constexpr int R = NROT / 64;
-        float4 csv[R > 0 ? R : 1][4];
-        if (NROT > 0 && p.rope_cs) {   // cos/sin written by the K/V prologue for this pass row
+    // Item state: the block entry and the lane's query row.
+    struct Item {
+        int q_row0, nq, q_pos0, k_row0, k_len, flag_row, h, kh, n_tiles;
+        const uint16_t *kbase, *vbase;
+    };
+    // The block entry is read with a scalar load: the compiler would read it with vector loads
+    // once the kernel has stored anything, and those would wait behind the in-flight tile fills.
+    auto decode = [&](int it) {
+        Item s;
+        const int bi = it / p.nh;
+        s.h = it - bi * p.nh;
+        const int32_t *blk = p.blocks + 8 * bi;
+        i32x8 e;
+        asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(e) : "s"(blk) : "memory");
+        s.q_row0 = e[0]; s.nq = e[1]; s.q_pos0 = e[2]; s.k_row0 = e[3]; s.k_len = e[4];
+        s.flag_row = e[5];
+        s.kh = s.h / (p.nh / p.nkv);
+        s.n_tiles = (s.k_len + BK - 1) / BK;
+        s.kbase = p.k_plane + ((size_t)s.kh * p.kvT + s.k_row0) * HD;
+        s.vbase = p.vt_plane + (size_t)s.kh * HD * p.kvT + s.k_row0;
+        return s;
+    };
+    auto load_tiles = [&](const Item &s, int kb, uint16_t *Ks, uint16_t *Vs) {
+        const char *kt_base = (const char *)(s.kbase + (size_t)kb * HD);
+        const char *vt_base = (const char *)(s.vbase + kb);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(kt_base + kfo[j]),
+                                             (lds_void *)(Ks + (wave_s * 4 + j) * 512), 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[j]),
+                                             (lds_void *)(Vs + (wave_s * 4 + j) * 512), 16, 0, 0);
+    };
+    // Q or gate rows of the block (128 x 256 bf16 = 64 KB, `off` 0 or HD within the head's
+    // 2*HD columns): rows 0-63 into G0, 64-127 into G1, slot s of a half = row s/32, 16-byte
+    // chunk (s%32) ^ (row & 15).
+    auto load_rows = [&](const Item &s, uint16_t *G0, uint16_t *G1, const int off) {
+        // An opaque copy of the lane id keeps this address math at each use: hoisted out of the
+        // item and tile loops, its 16 per-lane offsets would stay live and spill.
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int grp = wave_s * 8 + j;   // 64-slot group, 0..63
+            const int row = grp * 2 + (ln >> 5);
+            const int c = (ln & 31) ^ (row & 15);
+            int rc = min(row, s.nq - 1);
+            uint16_t *dst = (grp < 32 ? G0 : G1) + (grp & 31) * 512;
+            __builtin_amdgcn_global_load_lds((const void *)(p.qkv + ((size_t)s.q_row0 + rc) * p.row + (size_t)s.h * 2 * HD + off + c * 8),
+                                             (lds_void *)dst, 16, 0, 0);
+        }
+    };
+    // the row's rotary cos/sin, written by the K/V prologue for this pass row
+    float4 csv[R > 0 ? R : 1][4];
+    auto load_cs = [&](const Item &s) {
+        if (NROT > 0 && p.rope_cs) {
+            const int my_q = wave * ROWS + q16;
+            const size_t qrow = (size_t)s.q_row0 + (my_q < s.nq ? my_q : 0);
             const float *cs = p.rope_cs + qrow * (NROT / 2) * 2;
 #pragma unroll
             for (int c = 0; c < R; c++)
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) csv[c][q4] = *(const float4 *)(cs + 2 * (c * 32 + 8 * g) + 4 * q4);
         }
-        // The block's Q rows go to buffers 1 by DMA (1 KB per instruction, where per-lane loads
-        // of the B-operand chunks would touch 16 rows each); buffers 1 stay free until the first
-        // tile issues the second tile's fills, after this prologue's closing barrier.
-        load_rows(k1s, v1s, 0);
-        if (n_tiles > 0) load_tiles(0, k0s, v0s);
-        // The LDS store and reads of q_norm are issued as asm: the compiler would otherwise wait
-        // for the tile's global_load_lds fills (vmcnt(0)) before touching LDS.
-        const unsigned qn_addr = lds_addr((const uint16_t *)qn_lds);
+    };
+
+    // ---- first item's loads; q_norm (one element per thread) staged in LDS once
+    Item cur = decode(item);
+    {
+        const float qn_v = (p.q_norm && tid < HD) ? p.q_norm[tid] : 0.f;
+        load_cs(cur);
+        // The block's Q rows go to buffers 1 by DMA (1 KB per instruction); buffers 1 stay free
+        // until the first tile issues the second tile's fills, after the prologue's barrier.
+        load_rows(cur, k1s, v1s, 0);
+        if (cur.n_tiles > 0) load_tiles(cur, 0, k0s, v0s);
+        // The LDS store of q_norm is issued as asm: the compiler would otherwise wait for the
+        // tile's global_load_lds fills (vmcnt(0)) before touching LDS.
         if (tid < HD) asm volatile("ds_write_b32 %0, %1" : : "v"(qn_addr + 4u * tid), "v"(qn_v) : "memory");
-        __builtin_amdgcn_s_waitcnt(0);
-        __builtin_amdgcn_s_barrier();   // Q rows, q_norm and the first tile are in LDS
-        u32x4 qw[NC];
-        {
-            const uint16_t *qr = (my_q < 64 ? k1s : v1s) + (my_q & 63) * 256;
-#pragma unroll
-            for (int c = 0; c < NC; c++) qw[c] = *(const u32x4 *)(qr + (((4 * c + g) ^ (my_q & 15)) * 8));
-        }
-        float x[NC][8];
-        float ss = 0.f;
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                x[c][2 * j] = bf_lo(qw[c][j]);
-                x[c][2 * j + 1] = bf_hi(qw[c][j]);
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++) ss += x[c][j] * x[c][j];
-        }
-        ss = xrow_sum(ss);
-        if (p.q_norm) {   // NULL: no q/k norm (plain SDPA operands)
-            const float inv = rsqrtf(ss / (float)HD + p.eps);
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                bf16x8 r0 = lds_read16<0>(qn_addr + 4u * (c * 32 + 8 * g));
-                bf16x8 r1 = lds_read16<16>(qn_addr + 4u * (c * 32 + 8 * g));
-                lds_wait<0>(r0);
-                lds_wait<0>(r1);
-                const float4 w0 = __builtin_bit_cast(float4, r0), w1 = __builtin_bit_cast(float4, r1);
-                const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                for (int j = 0; j < 8; j++) x[c][j] = x[c][j] * inv * wn[j];
-            }
-        }
-        if (NROT > 0) {
-            // NeoX partial rotary: pair (i, i + NROT/2) sits in this lane at chunks c and c + R.
-            // Interleaved M-RoPE: pair i turns by axis i % 3 of pos3.
-            if (p.rope_cs) {
-#pragma unroll
-                for (int c = 0; c < R; c++) {
-                    const float t[16] = {csv[c][0].x, csv[c][0].y, csv[c][0].z, csv[c][0].w,
-                                         csv[c][1].x, csv[c][1].y, csv[c][1].z, csv[c][1].w,
-                                         csv[c][2].x, csv[c][2].y, csv[c][2].z, csv[c][2].w,
-                                         csv[c][3].x, csv[c][3].y, csv[c][3].z, csv[c][3].w};
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const float cs_ = t[2 * j], sn = t[2 * j + 1];
-                        const float x0 = x[c][j], x1 = x[c + R][j];
-                        x[c][j] = x0 * cs_ - x1 * sn;
-                        x[c + R][j] = x1 * cs_ + x0 * sn;
-                    }
-                }
-            } else {
-                const int32_t *pp = p.pos3 + 3 * qrow;
-                const float pt = (float)pp[0], ph = (float)pp[1], pw = (float)pp[2];
-#pragma unroll
-                for (int c = 0; c < R; c++) {
-                    const float4 f0 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g);
-                    const float4 f1 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g + 4);
-                    const float fr[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const int i = c * 32 + 8 * g + j;
-                        const int ax = i % 3;
-                        const float pos = ax == 0 ? pt : (ax == 1 ? ph : pw);
-                        float sn, cs;
-                        rope_sincos(pos * fr[j], &sn, &cs);
-                        const float x0 = x[c][j], x1 = x[c + R][j];
-                        x[c][j] = x0 * cs - x1 * sn;
-                        x[c + R][j] = x1 * cs + x0 * sn;
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-            u32x4 w = {pack_bf16(x[c][0], x[c][1]), pack_bf16(x[c][2], x[c][3]),
-                       pack_bf16(x[c][4], x[c][5]), pack_bf16(x[c][6], x[c][7])};
-            qf[c] = __builtin_bit_cast(bf16x8, w);
-        }
     }
 
-    f32x4 o[16];
+    for (int k = 0;; k++) {
+        const int my_q = wave * ROWS + q16;
+        const bool q_valid = my_q < cur.nq;
+        const int qpos = cur.q_pos0 + my_q;
+        const bool wave_live = wave * ROWS < cur.nq;
+        const int wave_last_pos = cur.q_pos0 + wave * ROWS + ROWS - 1;
+        const int k_len = cur.k_len, n_tiles = cur.n_tiles;
+
+        // ---- Q prologue: lane holds Q[my_q][c*32 + 8g + j], the B operand of chunk c.
+        bf16x8 qf[NC];
+        {
+            if (k > 0) load_cs(cur);   // its latency hides behind the wait for the DMA fills
+            __builtin_amdgcn_s_waitcnt(0);
+            __builtin_amdgcn_s_barrier();   // Q rows, q_norm and the first tile are in LDS
+            // addresses from an opaque lane id, so that they are not hoisted out of the item loop
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const int mq = wave_s * ROWS + (ln & 15), gg = ln >> 4;
+            u32x4 qw[NC];
+            {
+                const uint16_t *qr = (mq < 64 ? k1s : v1s) + (mq & 63) * 256;
 #pragma unroll
-    for (int mt = 0; mt < 16; mt++) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
-    const float sl2 = p.scale_log2;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tr && tid == 0) tr[4] = wall_clock64();
-    // Two tiles per trip: each call names its read and fill buffers statically.
-    auto tile = [&](const int t, auto BUF) {
-        constexpr int buf = decltype(BUF)::value;
-        uint16_t *const Vs = buf ? v1s : v0s, *const Kn = buf ? k0s : k1s, *const Vn = buf ? v0s : v1s;
-        const int kb = t * BK;
-        if (kb + BK > k_len) {   // WG-uniform: the block's last tile
-            zero_tail(kb, Vs);
-            __syncthreads();
-        }
-        if (t + 1 < n_tiles) load_tiles(kb + BK, Kn, Vn);
-        else if (p.gate) load_rows(Kn, Vn, HD);   // the idle buffers take the epilogue's gate rows
-        if (wave_live && (!p.causal || kb <= wave_last_pos)) {
-            // S^T: 32 MFMAs (4 key tiles x 8 dim chunks), chunk-major so consecutive products
-            // go to different accumulators. K operands are read DEPTH steps ahead of their
-            // product so the LDS latency overlaps the matrix work.
-            constexpr int DEPTH = 6, QK = 4 * NC;
-            f32x4 s[4];
-            bf16x8 ring[DEPTH];
-            static_for<DEPTH>([&](auto I) {
-                constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
-                ring[st] = lds_read16<buf * 2 * KTILE + (c >> 2) * 256>(ka[kt][c & 3]);
-            });
-            static_for<QK>([&](auto I) {
-                constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
-                constexpr int ahead = (QK - 1 - st) < (DEPTH - 1) ? (QK - 1 - st) : (DEPTH - 1);
-                bf16x8 a = ring[st % DEPTH];
-                lds_wait<ahead>(a);
-                if constexpr (c == 0) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[kt], 0, 0, 0);
-                if constexpr (st + DEPTH < QK) {
-                    constexpr int n = st + DEPTH, nkt = n & 3, nc = n >> 2;
-                    ring[st % DEPTH] = lds_read16<buf * 2 * KTILE + (nc >> 2) * 256>(ka[nkt][nc & 3]);
+                for (int c = 0; c < NC; c++) qw[c] = *(const u32x4 *)(qr + (((4 * c + gg) ^ (mq & 15)) * 8));
+            }
+            float x[NC][8];
+            float ss = 0.f;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    x[c][2 * j] = bf_lo(qw[c][j]);
+                    x[c][2 * j + 1] = bf_hi(qw[c][j]);
                 }
-            });
-            // first V operands, in flight during the softmax
-            auto vread = [&](auto I) {   // step st = 16 * kc + mt
-                constexpr int st = decltype(I)::value, mt = st & 15, kc = st >> 4;
-                constexpr int off = buf * 2 * VTILE + (32 * (mt >> 1) + 4 * (mt & 1)) * BK * 2;
-                return lds_read16<off>(kc ? va1 : va0);
-            };
-            bf16x8 vring[DEPTH];
-            static_for<DEPTH>([&](auto I) { vring[decltype(I)::value] = vread(I); });
-            // Online softmax in the exp2 domain. Masked scores are -inf, so their P is an exact
-            // zero and a tile past a row's diagonal rescales the row by exactly 1.
-            if ((kb + BK > k_len) || (p.causal && kb + BK - 1 > q_pos0 + wave * ROWS)) {
-                // element (kt, i) is key kb + 32(kt>>1) + 8g + 4(kt&1) + i
-                const int lim = min(k_len - 1, p.causal ? qpos : k_len - 1) - kb - 8 * g;
+#pragma unroll
+                for (int j = 0; j < 8; j++) ss += x[c][j] * x[c][j];
+            }
+            ss = xrow_sum(ss);
+            if (p.q_norm) {   // NULL: no q/k norm (plain SDPA operands)
+                const float inv = rsqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    bf16x8 r0 = lds_read16<0>(qn_addr + 4u * (c * 32 + 8 * gg));
+                    bf16x8 r1 = lds_read16<16>(qn_addr + 4u * (c * 32 + 8 * gg));
+                    lds_wait<0>(r0);
+                    lds_wait<0>(r1);
+                    const float4 w0 = __builtin_bit_cast(float4, r0), w1 = __builtin_bit_cast(float4, r1);
+                    const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                    for (int j = 0; j < 8; j++) x[c][j] = x[c][j] * inv * wn[j];
+                }
+            }
+            if (NROT > 0) {
+                // NeoX partial rotary: pair (i, i + NROT/2) sits in this lane at chunks c and c + R.
+                // Interleaved M-RoPE: pair i turns by axis i % 3 of pos3.
+                if (p.rope_cs) {
+#pragma unroll
+                    for (int c = 0; c < R; c++) {
+                        const float t[16] = {csv[c][0].x, csv[c][0].y, csv[c][0].z, csv[c][0].w,
+                                             csv[c][1].x, csv[c][1].y, csv[c][1].z, csv[c][1].w,
+                                             csv[c][2].x, csv[c][2].y, csv[c][2].z, csv[c][2].w,
+                                             csv[c][3].x, csv[c][3].y, csv[c][3].z, csv[c][3].w};
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            const float cs_ = t[2 * j], sn = t[2 * j + 1];
+                            const float x0 = x[c][j], x1 = x[c + R][j];
+                            x[c][j] = x0 * cs_ - x1 * sn;
+                            x[c + R][j] = x1 * cs_ + x0 * sn;
+                        }
+                    }
+                } else {
+                    const size_t qrow = (size_t)cur.q_row0 + (q_valid ? my_q : 0);
+                    const int32_t *pp = p.pos3 + 3 * qrow;
+                    const float pt = (float)pp[0], ph = (float)pp[1], pw = (float)pp[2];
+#pragma unroll
+                    for (int c = 0; c < R; c++) {
+                        const float4 f0 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g);
+                        const float4 f1 = *(const float4 *)(p.inv_freq + c * 32 + 8 * g + 4);
+                        const float fr[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            const int i = c * 32 + 8 * g + j;
+                            const int ax = i % 3;
+                            const float pos = ax == 0 ? pt : (ax == 1 ? ph : pw);
+                            float sn, cs;
+                            rope_sincos(pos * fr[j], &sn, &cs);
+                            const float x0 = x[c][j], x1 = x[c + R][j];
+                            x[c][j] = x0 * cs - x1 * sn;
+                            x[c + R][j] = x1 * cs + x0 * sn;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                u32x4 w = {pack_bf16(x[c][0], x[c][1]), pack_bf16(x[c][2], x[c][3]),
+                           pack_bf16(x[c][4], x[c][5]), pack_bf16(x[c][6], x[c][7])};
+                qf[c] = __builtin_bit_cast(bf16x8, w);
+            }
+        }
+
+        f32x4 o[16];
+#pragma unroll
+        for (int mt = 0; mt < 16; mt++) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float m_run = -INFINITY, l_run = 0.f;
+        const float sl2 = p.scale_log2;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();   // every wave has read its Q rows: buffers 1 may take the second tile
+        if (tr && tid == 0 && k == 0) tr[4] = wall_clock64();
+        auto zero_tail = [&](int kb, uint16_t *Vs) {   // V^T entries of keys >= k_len -> 0
+            const int valid = k_len - kb;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int s = tid + 512 * j;
+                const int d = s >> 3, c = (s & 7) ^ v_swz(d);
+                const int k0 = c * 8;
+                u32x4 w = *(u32x4 *)(Vs + s * 8);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const unsigned keep = (k0 + 2 * e + 1 < valid) ? 0xffffffffu : (k0 + 2 * e < valid ? 0xffffu : 0u);
+                    w[e] &= keep;
+                }
+                *(u32x4 *)(Vs + s * 8) = w;
+            }
+        };
+        // Two tiles per trip: each call names its read and fill buffers statically.
+        auto tile = [&](const int t, auto BUF) {
+            constexpr int buf = decltype(BUF)::value;
+            uint16_t *const Vs = buf ? v1s : v0s, *const Kn = buf ? k0s : k1s, *const Vn = buf ? v0s : v1s;
+            const int kb = t * BK;
+            if (kb + BK > k_len) {   // WG-uniform: the block's last tile
+                zero_tail(kb, Vs);
+                __syncthreads();
+            }
+            if (t + 1 < n_tiles) load_tiles(cur, kb + BK, Kn, Vn);
+            else if (p.gate) load_rows(cur, Kn, Vn, HD);   // the idle buffers take the epilogue's gate rows
+            if (wave_live && (!p.causal || kb <= wave_last_pos)) {
+                // S^T: 32 MFMAs (4 key tiles x 8 dim chunks), chunk-major so consecutive products
+                // go to different accumulators. K operands are read DEPTH steps ahead of their
+                // product so the LDS latency overlaps the matrix work.
+                constexpr int DEPTH = 6, QK = 4 * NC;
+                f32x4 s[4];
+                bf16x8 ring[DEPTH];
+                static_for<DEPTH>([&](auto I) {
+                    constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
+                    ring[st] = lds_read16<buf * 2 * KTILE + (c >> 2) * 256>(ka[kt][c & 3]);
+                });
+                static_for<QK>([&](auto I) {
+                    constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
+                    constexpr int ahead = (QK - 1 - st) < (DEPTH - 1) ? (QK - 1 - st) : (DEPTH - 1);
+                    bf16x8 a = ring[st % DEPTH];
+                    lds_wait<ahead>(a);
+                    if constexpr (c == 0) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[kt], 0, 0, 0);
+                    if constexpr (st + DEPTH < QK) {
+                        constexpr int n = st + DEPTH, nkt = n & 3, nc = n >> 2;
+                        ring[st % DEPTH] = lds_read16<buf * 2 * KTILE + (nc >> 2) * 256>(ka[nkt][nc & 3]);
+                    }
+                });
+                // first V operands, in flight during the softmax
+                auto vread = [&](auto I) {   // step st = 16 * kc + mt
+                    constexpr int st = decltype(I)::value, mt = st & 15, kc = st >> 4;
+                    constexpr int off = buf * 2 * VTILE + (32 * (mt >> 1) + 4 * (mt & 1)) * BK * 2;
+                    return lds_read16<off>(kc ? va1 : va0);
+                };
+                bf16x8 vring[DEPTH];
+                static_for<DEPTH>([&](auto I) { vring[decltype(I)::value] = vread(I); });
+                // Online softmax in the exp2 domain. Masked scores are -inf, so their P is an exact
+                // zero and a tile past a row's diagonal rescales the row by exactly 1.
+                if ((kb + BK > k_len) || (p.causal && kb + BK - 1 > cur.q_pos0 + wave * ROWS)) {
+                    // element (kt, i) is key kb + 32(kt>>1) + 8g + 4(kt&1) + i
+                    const int lim = min(k_len - 1, p.causal ? qpos : k_len - 1) - kb - 8 * g;
+#pragma unroll
+                    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            s[kt][i] = (32 * (kt >> 1) + 4 * (kt & 1) + i > lim) ? -INFINITY : s[kt][i];
+                }
+                float mx = -INFINITY;
 #pragma unroll
                 for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        s[kt][i] = (32 * (kt >> 1) + 4 * (kt & 1) + i > lim) ? -INFINITY : s[kt][i];
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kt][i]);
-            // The running max moves only when a tile's max passes it by more than 8 (log2 units):
-            // P stays below 2^8, and the O rescale below runs on few tiles. The lane's own max
-            // decides whether any row of the wave may move; only then is the row max reduced
-            // over the row's four lanes.
-            float mn = m_run;
-            if (__any(mx * sl2 > m_run + 8.f)) {
-                const float rmx = xrow_max(mx) * sl2;
-                mn = (rmx > m_run + 8.f) ? rmx : m_run;
-            }
-            const float msub = (mn == -INFINITY) ? 0.f : mn;
-            const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
-            float rs = 0.f;
-            bf16x8 pk[2];
-#pragma unroll
-            for (int kc = 0; kc < 2; kc++) {
-                unsigned w[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int kt = 2 * kc + (j >> 1), i = 2 * (j & 1);
-                    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][i], sl2, -msub));
-                    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][i + 1], sl2, -msub));
-                    w[j] = pack_bf16(p0, p1);
-                    // the row sum takes the rounded P that the PV product multiplies
-                    rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]),
-                                                         bf16x2{(__bf16)1.0f, (__bf16)1.0f}, rs, false);
+                    for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kt][i]);
+                // The running max moves only when a tile's max passes it by more than 8 (log2
+                // units): P stays below 2^8, and the O rescale below runs on few tiles. The lane's
+                // own max decides whether any row of the wave may move; only then is the row max
+                // reduced over the row's four lanes.
+                float mn = m_run;
+                if (__any(mx * sl2 > m_run + 8.f)) {
+                    const float rmx = xrow_max(mx) * sl2;
+                    mn = (rmx > m_run + 8.f) ? rmx : m_run;
                 }
-                u32x4 wv = {w[0], w[1], w[2], w[3]};
-                pk[kc] = __builtin_bit_cast(bf16x8, wv);
-            }
-            l_run = l_run * alpha + rs;   // the lane's share; the row's four lanes add up at the end
-            m_run = mn;
-            if (__any(alpha != 1.f)) {
+                const float msub = (mn == -INFINITY) ? 0.f : mn;
+                const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
+                float rs = 0.f;
+                bf16x8 pk[2];
 #pragma unroll
-                for (int mt = 0; mt < 16; mt++) o[mt] *= alpha;
+                for (int kc = 0; kc < 2; kc++) {
+                    unsigned w[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int kt = 2 * kc + (j >> 1), i = 2 * (j & 1);
+                        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][i], sl2, -msub));
+                        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][i + 1], sl2, -msub));
+                        w[j] = pack_bf16(p0, p1);
+                        // the row sum takes the rounded P that the PV product multiplies
+                        rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]),
+                                                             bf16x2{(__bf16)1.0f, (__bf16)1.0f}, rs, false);
+                    }
+                    u32x4 wv = {w[0], w[1], w[2], w[3]};
+                    pk[kc] = __builtin_bit_cast(bf16x8, wv);
+                }
+                l_run = l_run * alpha + rs;   // the lane's share; the row's four lanes add up at the end
+                m_run = mn;
+                if (__any(alpha != 1.f)) {
+#pragma unroll
+                    for (int mt = 0; mt < 16; mt++) o[mt] *= alpha;
+                }
+                static_for<32>([&](auto I) {   // O^T: 32 MFMAs over 16 rotating accumulators, same read-ahead
+                    constexpr int st = decltype(I)::value, mt = st & 15, kc = st >> 4;
+                    constexpr int ahead = (31 - st) < (DEPTH - 1) ? (31 - st) : (DEPTH - 1);
+                    bf16x8 a = vring[st % DEPTH];
+                    lds_wait<ahead>(a);
+                    o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[kc], o[mt], 0, 0, 0);
+                    if constexpr (st + DEPTH < 32) vring[st % DEPTH] = vread(std::integral_constant<int, st + DEPTH>{});
+                });
             }
-            static_for<32>([&](auto I) {   // O^T: 32 MFMAs over 16 rotating accumulators, same read-ahead
-                constexpr int st = decltype(I)::value, mt = st & 15, kc = st >> 4;
-                constexpr int ahead = (31 - st) < (DEPTH - 1) ? (31 - st) : (DEPTH - 1);
-                bf16x8 a = vring[st % DEPTH];
-                lds_wait<ahead>(a);
-                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[kc], o[mt], 0, 0, 0);
-                if constexpr (st + DEPTH < 32) vring[st % DEPTH] = vread(std::integral_constant<int, st + DEPTH>{});
-            });
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        };
+        for (int t = 0; t < n_tiles; t += 2) {
+            tile(t, std::integral_constant<int, 0>{});
+            if (t + 1 < n_tiles) tile(t + 1, std::integral_constant<int, 1>{});
         }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-    };
-    for (int t = 0; t < n_tiles; t += 2) {
-        tile(t, std::integral_constant<int, 0>{});
-        if (t + 1 < n_tiles) tile(t + 1, std::integral_constant<int, 1>{});
-    }
+        if (tr && tid == 0 && k == 0) tr[5] = wall_clock64();
 
-    if (tr && tid == 0) tr[5] = wall_clock64();
-    // ---- Epilogue: O / l times sigmoid(gate); lane (q16, g) holds dims 32u + 8g + [0, 8).
-    // The gate rows were loaded into the buffers the last tile left idle.
-    const uint16_t *gate0 = (n_tiles & 1) ? k1s : k0s, *gate1 = (n_tiles & 1) ? v1s : v0s;
-    const float l_row = xrow_sum(l_run);   // outside the row-divergent branch: lanes exchange values
-    if (q_valid) {
-        const float il = l_row > 0.f ? 1.f / l_row : 0.f;
-        const size_t t = (size_t)q_row0 + my_q;
-        int32_t *flag = p.ovf ? p.ovf + flag_row : nullptr;
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int d0 = 32 * u + 8 * g;
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v[i] = o[2 * u][i] * il;
-                v[4 + i] = o[2 * u + 1][i] * il;
+        // ---- Epilogue: O / l times sigmoid(gate); lane (q16, g) holds dims 32u + 8g + [0, 8).
+        // The gate rows sit in the buffers the last tile left idle (buffers 1 when the tile count
+        // is odd, 0 when even). The next item's loads whose buffers are free already (its first
+        // tile into buffers 0, or its Q rows into buffers 1) are issued before the epilogue, the
+        // other half once every wave has read its gate values.
+        const float l_row = xrow_sum(l_run);   // outside the row-divergent branch: lanes exchange values
+        const int gate_buf = n_tiles & 1;
+        const int q_row0 = cur.q_row0, flag_row = cur.flag_row, h = cur.h;
+        item = items.get(k + 1);
+        if (item >= 0) {
+            cur = decode(item);
+            if (gate_buf) {
+                if (cur.n_tiles > 0) load_tiles(cur, 0, k0s, v0s);
+            } else {
+                load_rows(cur, k1s, v1s, 0);
             }
-            if (p.gate) {
-                const int c = (4 * u + g) ^ (my_q & 15);
-                const uint16_t *grow = (my_q < 64 ? gate0 : gate1) + (my_q & 63) * 256;
-                const u32x4 gw = *(const u32x4 *)(grow + c * 8);
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    v[2 * j] *= sigmoidf(bf_lo(gw[j]));
-                    v[2 * j + 1] *= sigmoidf(bf_hi(gw[j]));
-                }
-            }
-            store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);
         }
+        if (q_valid) {
+            const float il = l_row > 0.f ? 1.f / l_row : 0.f;
+            const size_t t = (size_t)q_row0 + my_q;
+            int32_t *flag = p.ovf ? p.ovf + flag_row : nullptr;
+            // gate reads as asm: the compiler would wait for the in-flight fills before them
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const int mq = wave_s * ROWS + (ln & 15), gg = ln >> 4;
+            const unsigned gbase = lds_addr(gate_buf ? k1s : k0s) + (mq < 64 ? 0u : 2u * 2 * KTILE) + (unsigned)(mq & 63) * 512u;
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int d0 = 32 * u + 8 * g;
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    v[i] = o[2 * u][i] * il;
+                    v[4 + i] = o[2 * u + 1][i] * il;
+                }
+                if (p.gate) {
+                    bf16x8 gr = lds_read16<0>(gbase + (unsigned)(((4 * u + gg) ^ (mq & 15)) * 16));
+                    lds_wait<0>(gr);
+                    const u32x4 gw = __builtin_bit_cast(u32x4, gr);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        v[2 * j] *= sigmoidf(bf_lo(gw[j]));
+                        v[2 * j + 1] *= sigmoidf(bf_hi(gw[j]));
+                    }
+                }
+                store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);
+            }
+        }
+        if (item >= 0) {
+            // every wave has read its gate values (each read waited for): their buffers are free.
+            // A bare barrier: a fence would also wait for the stores and the fills in flight.
+            __builtin_amdgcn_s_barrier();
+            if (gate_buf) {
+                load_rows(cur, k1s, v1s, 0);
+            } else {
+                if (cur.n_tiles > 0) load_tiles(cur, 0, k0s, v0s);
+            }
+        }
+        if (item < 0) break;
     }
 }
 
-// Grid: one workgroup per (query block, q head) work item.
+// Grid: G workgroups; workgroup b runs the items ItemList assigns it (one each when G is the
+// item count, several when G is the CU count).
 template <int NROT>
 __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t smem[text::LDS_ELEMS];
     __shared__ __attribute__((aligned(16))) float qn_lds[text::HD];
     uint64_t t0 = 0;
     if (p.trace && threadIdx.x == 0) t0 = wall_clock64();
-    int bi, h;
-    if (p.xcd_heads) {
-        // Workgroup ids go round-robin over the 8 XCDs (each with its own L2). XCD x takes heads
-        // x*xcd_heads .. +xcd_heads-1 of every block, so it streams the K/V of as few KV heads
-        // as possible; blocks stay in the plan's longest-first order.
-        const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
-        bi = j / p.xcd_heads;
-        h = x * p.xcd_heads + (j - bi * p.xcd_heads);
-    } else {
-        bi = blockIdx.x / p.nh;
-        h = blockIdx.x - bi * p.nh;
-    }
     uint64_t *tr = p.trace ? p.trace + 8 * blockIdx.x : nullptr;
-    text_block<NROT>(p, bi, h, smem, qn_lds, tr);
+    text_items<NROT>(p, smem, qn_lds, tr);
     if (tr && threadIdx.x == 0) {
-        // per-workgroup trace (100 MHz wall clock): start, end, hardware id, XCC id; the block
-        // wrote the end of its prologue and of its key loop into slots 4 and 5
+        // per-workgroup trace (100 MHz wall clock): start, end, hardware id, XCC id; the first
+        // item wrote the end of its prologue and of its key loop into slots 4 and 5
         tr[0] = t0;
         tr[1] = wall_clock64();
         tr[2] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
