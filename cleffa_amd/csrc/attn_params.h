@@ -23,7 +23,7 @@ struct AttnParams {
     int causal, gate, out_type, out_ld;
     int n_blk;                // blocks in the plan (work items = n_blk * nh)
     int xcd_heads;            // nh / 8 when heads split evenly over the 8 XCDs, else 0
-    uint64_t *trace;          // NULL, or [grid][8] per-workgroup start, end, HW_ID, XCC_ID, prologue end, loop end
+    uint64_t *trace;          // NULL, or [n_blk * nh][8] per work item: start, end, HW_ID, XCC_ID, prologue end, loop end, workgroup, ordinal
 };
 
 struct PrepParams {

@@ -127,7 +127,7 @@ struct ItemList {
 // next item's Q rows and first K / V^T tile load by DMA into the LDS buffers the finished key loop
 // left free, and its rotary cos/sin into registers.
 template <int NROT>
-__device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, float *qn_lds, uint64_t *tr) {
+__device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, float *qn_lds) {
     using namespace text;
     static_assert(NROT % 64 == 0 && NROT <= HD, "rotary pairs must sit in one lane");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -255,6 +255,16 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     }
 
     for (int k = 0;; k++) {
+        // trace row of this item (100 MHz wall clock): start, end, HW_ID, XCC_ID, prologue end,
+        // key loop end, workgroup, ordinal within the workgroup
+        uint64_t *const tr = (p.trace && tid == 0) ? p.trace + 8 * (size_t)item : nullptr;
+        if (tr) {
+            tr[0] = wall_clock64();
+            tr[2] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+            tr[3] = __builtin_amdgcn_s_getreg((15 << 11) | 20);
+            tr[6] = blockIdx.x;
+            tr[7] = k;
+        }
         const int my_q = wave * ROWS + q16;
         const bool q_valid = my_q < cur.nq;
         const int qpos = cur.q_pos0 + my_q;
@@ -361,7 +371,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         const float sl2 = p.scale_log2;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();   // every wave has read its Q rows: buffers 1 may take the second tile
-        if (tr && tid == 0 && k == 0) tr[4] = wall_clock64();
+        if (tr) tr[4] = wall_clock64();
         auto zero_tail = [&](int kb, uint16_t *Vs) {   // V^T entries of keys >= k_len -> 0
             const int valid = k_len - kb;
 #pragma unroll
@@ -487,7 +497,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             tile(t, std::integral_constant<int, 0>{});
             if (t + 1 < n_tiles) tile(t + 1, std::integral_constant<int, 1>{});
         }
-        if (tr && tid == 0 && k == 0) tr[5] = wall_clock64();
+        if (tr) tr[5] = wall_clock64();
 
         // ---- Epilogue: O / l times sigmoid(gate); lane (q16, g) holds dims 32u + 8g + [0, 8).
         // The gate rows sit in the buffers the last tile left idle (buffers 1 when the tile count
@@ -547,6 +557,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                 if (cur.n_tiles > 0) load_tiles(cur, 0, k0s, v0s);
             }
         }
+        if (tr) tr[1] = wall_clock64();
         if (item < 0) break;
     }
 }
@@ -557,18 +568,7 @@ template <int NROT>
 __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t smem[text::LDS_ELEMS];
     __shared__ __attribute__((aligned(16))) float qn_lds[text::HD];
-    uint64_t t0 = 0;
-    if (p.trace && threadIdx.x == 0) t0 = wall_clock64();
-    uint64_t *tr = p.trace ? p.trace + 8 * blockIdx.x : nullptr;
-    text_items<NROT>(p, smem, qn_lds, tr);
-    if (tr && threadIdx.x == 0) {
-        // per-workgroup trace (100 MHz wall clock): start, end, hardware id, XCC id; the first
-        // item wrote the end of its prologue and of its key loop into slots 4 and 5
-        tr[0] = t0;
-        tr[1] = wall_clock64();
-        tr[2] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
-        tr[3] = __builtin_amdgcn_s_getreg((15 << 11) | 20);
-    }
+    text_items<NROT>(p, smem, qn_lds);
 }
 
 }  // namespace clef_hip

@@ -111,10 +111,11 @@ typedef struct {
     int out_type;             /* CLEF_HIP_OUT_* */
     float f16_lim;            /* overflow limit for CLEF_HIP_OUT_F16 (65504) */
     int32_t *ovf;             /* [T] int32 flags, set at the record's first pass row; may be NULL */
-    uint64_t *trace;          /* NULL, or [grid][8] u64 per attention workgroup: start, end (100 MHz
-                                 device wall clock), HW_ID and XCC_ID registers, end of the
-                                 prologue, end of the key loop; the CLEF_PROFILE analogue
-                                 (clef_metal.m:52-68) at workgroup grain */
+    uint64_t *trace;          /* NULL, or [n_blk * nh][8] u64 per work item (query block, q head):
+                                 start, end (100 MHz device wall clock), HW_ID and XCC_ID
+                                 registers, end of the prologue, end of the key loop, workgroup,
+                                 ordinal in the workgroup; the CLEF_PROFILE analogue
+                                 (clef_metal.m:52-68) at work-item grain */
 } clef_hip_attn_args;
 
 /* K/V prologue only: RMSNorm + rotary of each pass row's K into its plane row (kv_tok), V into
