@@ -78,7 +78,7 @@ def build_step(cfg, seed):
     att = TextAttention(w["nh"], w["nkv"], w["hd"], w["n_rot"], rope_theta=w["theta"], device=dev)
     if cfg == "C3":
         plan = AttnPlan(w["cu_seqlens"], w["cu_seqlens_k"], causal=True, device=dev)
-        kp = w["k_cache"].contiguous()
+        kp = w["k_cache"].half().contiguous()   # f16 K plane
         vt = w["v_cache"].transpose(1, 2).contiguous()
         kvT = kp.shape[1]
     else:

@@ -171,8 +171,8 @@ class TextAttention:
             if n_rot else torch.zeros(1, dtype=torch.float32, device=self.device)
 
     def planes(self, kvT):
-        """K plane [nkv][kvT][hd] and V^T plane [nkv][hd][kvT] (bf16)."""
-        k = torch.empty((self.nkv, kvT, self.hd), dtype=torch.bfloat16, device=self.device)
+        """K plane [nkv][kvT][hd] (f16) and V^T plane [nkv][hd][kvT] (bf16)."""
+        k = torch.empty((self.nkv, kvT, self.hd), dtype=torch.float16, device=self.device)
         vt = torch.empty((self.nkv, self.hd, kvT), dtype=torch.bfloat16, device=self.device)
         return k, vt
 
@@ -194,7 +194,7 @@ class TextAttention:
             _check(k_norm, "k_norm", (self.hd,), torch.float32, dev)
         if self.n_rot:
             _check(pos3, "pos3", (T, 3), torch.int32, dev)
-        _check(k_plane, "k_plane", (self.nkv, kvT, self.hd), torch.bfloat16, dev)
+        _check(k_plane, "k_plane", (self.nkv, kvT, self.hd), torch.float16, dev)
         _check(vt_plane, "vt_plane", (self.nkv, self.hd, kvT), torch.bfloat16, dev)
         if kvT < plan.kv_rows or kvT % 8:
             raise ValueError(f"kvT {kvT} must be >= {plan.kv_rows} and a multiple of 8")

@@ -80,12 +80,8 @@ bool check_text(const clef_hip_attn_args *a, bool need_core, char *err, size_t e
 // loads overlap the current one's epilogue (measured 2-3% faster at C1, 1% at C2), or one
 // workgroup per item with CLEF_HIP_TEXT_PERSISTENT=0.
 bool text_persistent() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("CLEF_HIP_TEXT_PERSISTENT");
-        v = (e && e[0] == '0') ? 0 : 1;
-    }
-    return v == 1;
+    const char *e = getenv("CLEF_HIP_TEXT_PERSISTENT");
+    return !(e && e[0] == '0');
 }
 
 long device_cus() {

@@ -15,6 +15,8 @@ namespace clef_hip {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
 typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
 
@@ -25,6 +27,11 @@ __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((unsi
 // Round-to-nearest-even pair conversion (v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
     bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(unsigned, v);
+}
+// Round-to-nearest-even pair conversion to f16 (the text path's Q and K operands).
+__device__ __forceinline__ unsigned pack_f16(float a, float b) {
+    f16x2 v = {(_Float16)a, (_Float16)b};
     return __builtin_bit_cast(unsigned, v);
 }
 __device__ __forceinline__ uint16_t f2bf(float a) {
@@ -99,7 +106,7 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 // ------------------------------------------------------------------------------------------
 // Text K/V prologue (metal/clef.metal:245-300 and 873-928 for K and V): K = RMSNorm(k) * (1+w)
-// then partial rotary into the K plane [nkv][kvT][HD]; V unnormalised into the V^T plane
+// then partial rotary into the f16 K plane [nkv][kvT][HD]; V unnormalised into the V^T plane
 // [nkv][HD][kvT]; the rotary cos/sin of each pass row into rope_cs for the Q prologue.
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ float row16_sum(float v) {   // sum over the lane's 16-lane row
@@ -210,7 +217,7 @@ __global__ __launch_bounds__(16 * kPrepRows) void text_prep_kv_kernel(PrepParams
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const float *xs = x + 8 * h;
-            u32x4 ko = {pack_bf16(xs[0], xs[1]), pack_bf16(xs[2], xs[3]), pack_bf16(xs[4], xs[5]), pack_bf16(xs[6], xs[7])};
+            u32x4 ko = {pack_f16(xs[0], xs[1]), pack_f16(xs[2], xs[3]), pack_f16(xs[4], xs[5]), pack_f16(xs[6], xs[7])};
             *(u32x4 *)(dst + 8 * h) = ko;
         }
     }

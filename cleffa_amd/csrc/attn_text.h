@@ -8,9 +8,14 @@
 // Workgroup: 8 wavefronts (2 per SIMD), one block of 128 query rows of one q head; wave w owns
 // rows 16w .. 16w+15. Everything per wave lives in ~170 VGPRs (O^T 64, Q 32, S 16), so two
 // waves share a SIMD and one wave's softmax overlaps the other's matrix work.
-//   S^T = K . Q^T      v_mfma_f32_16x16x32_bf16: A = 16 keys x 32 dims of K from LDS,
-//                      B = the wave's Q (registers). A lane owns one query column.
-//   O^T += V^T . P^T   A = 16 dims x 32 keys of V^T from LDS, B = P straight from registers.
+//   S^T = K . Q^T      v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K from LDS,
+//                      B = the wave's Q (registers). A lane owns one query column. Q and K are
+//                      f16: their 11-bit significands keep the scores of sharp rows within the
+//                      output tolerance, where bf16-rounded K alone misses it (the normalised
+//                      values are bounded by 16 max|w|, far inside f16's range; without the
+//                      norms, Q and K must lie within it).
+//   O^T += V^T . P^T   v_mfma_f32_16x16x32_bf16: A = 16 dims x 32 keys of V^T (bf16) from LDS,
+//                      B = P (bf16) straight from registers.
 // The A rows are read in a permuted order (key / dim 8*(r/4) + 4*(tile&1) + r%4 for row r) so
 // that the 8 keys a lane's P covers and the 8 dims its O covers are consecutive: P is the next
 // product's B operand with no shuffle, and the epilogue stores 16-byte runs.
@@ -273,7 +278,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         const int k_len = cur.k_len, n_tiles = cur.n_tiles;
 
         // ---- Q prologue: lane holds Q[my_q][c*32 + 8g + j], the B operand of chunk c.
-        bf16x8 qf[NC];
+        f16x8 qf[NC];
         {
             if (k > 0) load_cs(cur);   // its latency hides behind the wait for the DMA fills
             __builtin_amdgcn_s_waitcnt(0);
@@ -358,9 +363,9 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             }
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                u32x4 w = {pack_bf16(x[c][0], x[c][1]), pack_bf16(x[c][2], x[c][3]),
-                           pack_bf16(x[c][4], x[c][5]), pack_bf16(x[c][6], x[c][7])};
-                qf[c] = __builtin_bit_cast(bf16x8, w);
+                u32x4 w = {pack_f16(x[c][0], x[c][1]), pack_f16(x[c][2], x[c][3]),
+                           pack_f16(x[c][4], x[c][5]), pack_f16(x[c][6], x[c][7])};
+                qf[c] = __builtin_bit_cast(f16x8, w);
             }
         }
 
@@ -416,7 +421,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                     bf16x8 a = ring[st % DEPTH];
                     lds_wait<ahead>(a);
                     if constexpr (c == 0) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[c], s[kt], 0, 0, 0);
+                    s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), qf[c], s[kt], 0, 0, 0);
                     if constexpr (st + DEPTH < QK) {
                         constexpr int n = st + DEPTH, nkt = n & 3, nc = n >> 2;
                         ring[st % DEPTH] = lds_read16<buf * 2 * KTILE + (nc >> 2) * 256>(ka[nkt][nc & 3]);

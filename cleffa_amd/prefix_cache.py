@@ -1,7 +1,7 @@
 """A prefix-cache entry's attention planes (clef_metal.m:15-29 struct clef_gpu_prefix,
 762-805 prefix_reserve), on torch device memory, grown and copied through the C ABI.
 
-Per attention layer the entry holds K [nkv][cap][hd] and V^T [nkv][hd][cap] bf16, indexed by the
+Per attention layer the entry holds K [nkv][cap][hd] (f16) and V^T [nkv][hd][cap] (bf16), indexed by the
 record's own token rows. A prefix pass over tokens L..T-1 of the record passes them to
 TextAttention.forward as k_plane / vt_plane with kvT = cap and cu_seqlens_k = [0, T]."""
 import ctypes
@@ -33,7 +33,7 @@ class PrefixEntry:
             return False
         if keep > self.cap:
             raise ValueError(f"keep {keep} exceeds the entry's {self.cap} rows")
-        K = [torch.empty(self.nkv, cap, self.hd, dtype=torch.bfloat16, device=self.device) for _ in range(self.n_layers)]
+        K = [torch.empty(self.nkv, cap, self.hd, dtype=torch.float16, device=self.device) for _ in range(self.n_layers)]
         Vt = [torch.empty(self.nkv, self.hd, cap, dtype=torch.bfloat16, device=self.device) for _ in range(self.n_layers)]
         err = ctypes.create_string_buffer(256)
         s = _stream_handle(stream)

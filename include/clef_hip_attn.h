@@ -14,11 +14,12 @@
  * with respect to the host and not reentrant for buffers they share. Nothing here allocates
  * device memory: the caller owns every buffer (clef_metal.m:337-412 ownership model).
  *
- * Layouts (bf16 = raw uint16 bits):
+ * Layouts (bf16 / f16 = raw uint16 bits):
  *   qkv     [T][row] bf16, the fused projection row: [nh x (query hd | gate hd)] [nkv x hd K]
  *           [nkv x hd V] (tools/convert.py:23-25, metal/clef.metal:245-248).
  *   pos3    [T][3] int32 rotary positions per pass row (temporal, grid row, grid column).
- *   K plane [nkv][kvT][hd] bf16, normalised and rotated keys, one row per key.
+ *   K plane [nkv][kvT][hd] f16, normalised and rotated keys, one row per key (f16: the scores
+ *           of sharp rows need its 11-bit significand to stay within tolerance).
  *   V^T     [nkv][hd][kvT] bf16, values transposed (keys contiguous per head dim).
  *   out     [T][nh*hd] (text) or [P][heads*hd] (vision): the o_proj operand, bf16 / f16 / f32.
  *   The plan (clef_hip_attn_plan) maps records to query blocks and kv rows; it is built once per
@@ -216,7 +217,7 @@ bool clef_hip_omni_attention(const clef_hip_omni_attn_args *a, void *stream, cha
 
 /* Prefix-cache entry planes (clef_metal.m:15-29 struct clef_gpu_prefix, 762-805 prefix_reserve).
  * An entry holds, per attention layer, a K plane [nkv][cap][hd] and a V^T plane [nkv][hd][cap],
- * bf16, rows (columns of V^T) indexed by the record's own token index; a prefix pass uses them as
+ * K f16 and V^T bf16, rows (columns of V^T) indexed by the record's own token index; a prefix pass uses them as
  * k_plane / vt_plane with kvT = cap and cu_seqlens_k = {0, L + n}. The caller allocates them.
  *
  * clef_hip_prefix_capacity: the capacity an entry of cur_cap rows needs to hold `rows` tokens:

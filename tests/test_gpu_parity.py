@@ -25,6 +25,18 @@ def test_config_full(name):
     _say(f"[parity] {name}: max_abs {mx:.3g} mean_abs {mean:.3g} blocks {plan.n_blk}")
 
 
+@pytest.mark.parametrize("seed", [1, 2, 3, 4, 5])
+def test_c1_more_seeds(seed):
+    """C1 at other seeds: its 2% outlier channels make some rows sharp, where bf16-rounded K
+    scores miss the max-abs bound (0.022-0.024 on two of these seeds, in a CPU emulation) and
+    the f16 Q/K operands keep it (0.008-0.013)."""
+    _say(f"[parity] C1 seed={seed}")
+    w = workloads.config("C1", seed=seed)
+    out, _ = gpu_text(w)
+    mx, mean = assert_close(out.float().cpu().numpy(), oracle_text(w), what=f"C1 seed {seed}")
+    _say(f"[parity] C1 seed {seed}: max_abs {mx:.3g} mean_abs {mean:.3g}")
+
+
 def test_c2_sampled_rows():
     """C2 (16,384-token causal request): float64 oracle on 96 sampled rows, every head."""
     _say("[parity] C2 sampled rows")
@@ -44,7 +56,7 @@ def test_c3_prefix():
     nh, nkv, hd = w["nh"], w["nkv"], w["hd"]
     att = TextAttention(nh, nkv, hd, 64, rope_theta=1e7)
     plan = AttnPlan(w["cu_seqlens"], w["cu_seqlens_k"], causal=True)
-    kp = w["k_cache"].cuda().contiguous()
+    kp = w["k_cache"].cuda().half().contiguous()   # the K plane is f16; bf16 values convert exactly
     vt = w["v_cache"].cuda().transpose(1, 2).contiguous()
     kvT = kp.shape[1]
     out = att.forward(w["qkv"].cuda(), w["q_norm"].cuda(), w["k_norm"].cuda(), w["pos3"].cuda(), plan,
@@ -69,7 +81,7 @@ def test_c3_prefix():
     for r in range(len(cq) - 1):
         n = cq[r + 1] - cq[r]
         cached = ck[r + 1] - n - ck[r]
-        assert np.array_equal(kp_h[:, ck[r]:ck[r] + cached], w["k_cache"].float().numpy()[:, ck[r]:ck[r] + cached])
+        assert np.array_equal(kp_h[:, ck[r]:ck[r] + cached], w["k_cache"].half().float().numpy()[:, ck[r]:ck[r] + cached])
     _say(f"[parity] C3: max_abs {mx:.3g} mean_abs {mean:.3g}")
 
 
@@ -239,3 +251,23 @@ def test_vision_mixed_images_and_f16():
         out = vis.forward(qkv.cuda(), None, torch.from_numpy(pos2).cuda(), plan, out_dtype=dt)
         torch.cuda.synchronize()
         assert_close(out.float().cpu().numpy(), want, what=f"vision {dt}")
+
+
+@pytest.mark.parametrize("nh,nkv,lengths", [
+    (24, 4, [1160, 890, 730, 425, 472, 136, 179, 104]),   # C1 shape: 864 items over the CUs
+    (12, 4, [300, 77, 1030]),                              # heads not a multiple of 8: plain snake order
+    (4, 1, [40, 3]),                                       # fewer items than CUs
+])
+def test_persistent_grid_matches_one_item_per_workgroup(nh, nkv, lengths, monkeypatch):
+    """The persistent grid (one workgroup per CU looping over its items) and one workgroup per
+    item give the same bytes: each item's arithmetic does not depend on where it runs."""
+    _say(f"[invariance] persistent grid nh={nh} nkv={nkv} lengths={lengths}")
+    w = workloads.text_inputs(lengths, nh, nkv, seed=31)
+    w.update(gate=True, theta=1e7)
+    monkeypatch.setenv("CLEF_HIP_TEXT_PERSISTENT", "1")
+    a, _ = gpu_text(w)
+    monkeypatch.setenv("CLEF_HIP_TEXT_PERSISTENT", "0")
+    b, _ = gpu_text(w)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    if sum(lengths) <= 1500:
+        assert_close(a.float().cpu().numpy(), oracle_text(w), what="persistent grid")
