@@ -48,8 +48,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3", "C4", "P", "O", "G"],
-                    help="C1-C4: attention configurations; P: prefix-cache growth copy (HBM-bound); "
+    ap.add_argument("--config", default="C1", choices=["C0", "C1", "C2", "C3", "C4", "P", "O", "G"],
+                    help="C0-C4: attention configurations; P: prefix-cache growth copy (HBM-bound); "
                          "O: Omni attention (hd 128, FP32, 16,344 tokens); G: the QKV and o_proj GEMMs around C1")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -96,7 +96,9 @@ def build_step(cfg, seed):
     nbytes = T * (2 * nh + 2 * nkv) * hd * 2 + T * nh * hd * 2
     if cfg == "C3":
         nbytes += 2 * nkv * (int(w["cu_seqlens_k"][-1]) - T) * hd * 2
-    names = {"C1": "C1 packed varlen causal micro-batch: 8 records, 4,096 tokens, 24/4 heads, hd 256, "
+    names = {"C0": "C0 one causal 1,024-token record, 16/4 heads, hd 256, plain SDPA operands (no norm, "
+                   "rotary or gate)",
+             "C1": "C1 packed varlen causal micro-batch: 8 records, 4,096 tokens, 24/4 heads, hd 256, "
                    "fused q/k RMSNorm + rotary(64, theta 1e7) + sigmoid gate",
              "C2": "C2 single causal request: 16,384 tokens, 24/4 heads, hd 256, fused prologue/gate",
              "C3": "C3 prefix-cache continuation: 4 x (2,048 cached + 512 new), 16/4 heads, hd 256"}
@@ -144,12 +146,15 @@ def cpu_baseline(w, cfg):
     from oracle import oracle
     qkv = w["qkv"].float().cpu().numpy()
     nh, nkv, hd, n_rot = w["nh"], w["nkv"], w["hd"], w["n_rot"]
-    inv = rope_inv_freq(w["theta"], n_rot)
-    qn, kn, pos = w["q_norm"].cpu().numpy(), w["k_norm"].cpu().numpy(), w["pos3"].cpu().numpy()
+    inv = rope_inv_freq(w["theta"], n_rot) if n_rot else None
+    qn = None if w["q_norm"] is None else w["q_norm"].cpu().numpy()
+    kn = None if w["k_norm"] is None else w["k_norm"].cpu().numpy()
+    pos = w["pos3"].cpu().numpy()
 
     def run():
         Q, K, V, G = oracle.text_prep(qkv, nh, nkv, hd, n_rot, qn, kn, pos, inv, precision="f32")
-        oracle.attention(Q, K, V, w["cu_seqlens"], None, True, hd ** -0.5, G, precision="f32")
+        oracle.attention(Q, K, V, w["cu_seqlens"], None, True, hd ** -0.5, G if w["gate"] else None,
+                         precision="f32")
 
     run()
     times = []
@@ -339,6 +344,14 @@ def main():
                                "cores": threads, "kind": "port",
                                "sample": "the full C1 step (prologue + attention, 4,096 tokens) in fp32, "
                                          "median of 5 runs"}
+        # the reference's CPU configuration (C0: one causal 1,024-token record, 16/4 heads, plain
+        # SDPA operands), timed the same way
+        from cleffa_amd import workloads
+        w0 = workloads.config("C0", seed=a.seed)
+        sec0, _ = cpu_baseline(w0, "C0")
+        f0 = 4.0 * 256 * 16 * (1024 * 1025 // 2)
+        res["cpu_baseline"]["c0"] = {"ms": round(sec0 * 1e3, 2), "tflops": round(f0 / sec0 / 1e12, 5),
+                                     "gflop": round(f0 / 1e9, 3)}
     print(json.dumps(res), flush=True)
 
 
