@@ -530,8 +530,15 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             asm volatile("" : "+v"(ln));
             const int mq = wave_s * ROWS + (ln & 15), gg = ln >> 4;
             const unsigned gbase = lds_addr(gate_buf ? k1s : k0s) + (mq < 64 ? 0u : 2u * 2 * KTILE) + (unsigned)(mq & 63) * 512u;
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
+            // gate chunks read two ahead of their use (a ring of 3), the last waits draining it
+            bf16x8 gring[3];
+            auto gread = [&](int u) { return lds_read16<0>(gbase + (unsigned)(((4 * u + gg) ^ (mq & 15)) * 16)); };
+            if (p.gate) {
+                gring[0] = gread(0);
+                gring[1] = gread(1);
+            }
+            static_for<8>([&](auto U) {
+                constexpr int u = decltype(U)::value;
                 const int d0 = 32 * u + 8 * g;
                 float v[8];
 #pragma unroll
@@ -540,8 +547,9 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                     v[4 + i] = o[2 * u + 1][i] * il;
                 }
                 if (p.gate) {
-                    bf16x8 gr = lds_read16<0>(gbase + (unsigned)(((4 * u + gg) ^ (mq & 15)) * 16));
-                    lds_wait<0>(gr);
+                    if constexpr (u + 2 < 8) gring[(u + 2) % 3] = gread(u + 2);
+                    bf16x8 gr = gring[u % 3];
+                    lds_wait<(u + 2 < 8) ? 2 : (u + 1 < 8 ? 1 : 0)>(gr);
                     const u32x4 gw = __builtin_bit_cast(u32x4, gr);
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
@@ -550,7 +558,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                     }
                 }
                 store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);
-            }
+            });
         }
         if (item >= 0) {
             // every wave has read its gate values (each read waited for): their buffers are free.
