@@ -185,13 +185,10 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     };
     // The block entry is read with a scalar load: the compiler would read it with vector loads
     // once the kernel has stored anything, and those would wait behind the in-flight tile fills.
-    auto decode = [&](int it) {
+    auto decode_from = [&](const i32x8 &e, int it) {
         Item s;
         const int bi = it / p.nh;
         s.h = it - bi * p.nh;
-        const int32_t *blk = p.blocks + 8 * bi;
-        i32x8 e;
-        asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(e) : "s"(blk) : "memory");
         s.q_row0 = e[0]; s.nq = e[1]; s.q_pos0 = e[2]; s.k_row0 = e[3]; s.k_len = e[4];
         s.flag_row = e[5];
         s.kh = s.h / (p.nh / p.nkv);
@@ -199,6 +196,11 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         s.kbase = p.k_plane + ((size_t)s.kh * p.kvT + s.k_row0) * HD;
         s.vbase = p.vt_plane + (size_t)s.kh * HD * p.kvT + s.k_row0;
         return s;
+    };
+    auto decode = [&](int it) {
+        i32x8 e;
+        asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(e) : "s"(p.blocks + 8 * (it / p.nh)) : "memory");
+        return decode_from(e, it);
     };
     auto load_tiles = [&](const Item &s, int kb, uint16_t *Ks, uint16_t *Vs) {
         const char *kt_base = (const char *)(s.kbase + (size_t)kb * HD);
@@ -247,12 +249,15 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
 
     // ---- first item's loads; q_norm (one element per thread) staged in LDS once
     Item cur = decode(item);
+    // Buffers of an item: its Q rows arrive in pair `qb`, its first key tile in the other pair
+    // (`par`), and the tiles alternate from there. The Q rows are issued first, then the rotary
+    // cos/sin, then the first tile (8 loads per wave), so the prologue waits for the Q rows alone
+    // and rotates them while the tile lands.
+    int par = 0;
     {
         const float qn_v = (p.q_norm && tid < HD) ? p.q_norm[tid] : 0.f;
-        load_cs(cur);
-        // The block's Q rows go to buffers 1 by DMA (1 KB per instruction); buffers 1 stay free
-        // until the first tile issues the second tile's fills, after the prologue's barrier.
         load_rows(cur, k1s, v1s, 0);
+        load_cs(cur);
         if (cur.n_tiles > 0) load_tiles(cur, 0, k0s, v0s);
         // The LDS store of q_norm is issued as asm: the compiler would otherwise wait for the
         // tile's global_load_lds fills (vmcnt(0)) before touching LDS.
@@ -279,17 +284,19 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
 
         // ---- Q prologue: lane holds Q[my_q][c*32 + 8g + j], the B operand of chunk c.
         f16x8 qf[NC];
+        const int nxt = items.get(k + 1);
+        i32x8 ne;
         {
-            if (k > 0) load_cs(cur);   // its latency hides behind the wait for the DMA fills
-            __builtin_amdgcn_s_waitcnt(0);
-            __builtin_amdgcn_s_barrier();   // Q rows, q_norm and the first tile are in LDS
+            // the Q rows and q_norm are in LDS once the first tile's 8 loads are all that remain
+            if (cur.n_tiles > 0) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
             // addresses from an opaque lane id, so that they are not hoisted out of the item loop
             int ln = lane;
             asm volatile("" : "+v"(ln));
             const int mq = wave_s * ROWS + (ln & 15), gg = ln >> 4;
             u32x4 qw[NC];
             {
-                const uint16_t *qr = (mq < 64 ? k1s : v1s) + (mq & 63) * 256;
+                const uint16_t *qr = (mq < 64 ? (par ? k0s : k1s) : (par ? v0s : v1s)) + (mq & 63) * 256;
 #pragma unroll
                 for (int c = 0; c < NC; c++) qw[c] = *(const u32x4 *)(qr + (((4 * c + gg) ^ (mq & 15)) * 8));
             }
@@ -374,8 +381,13 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         for (int mt = 0; mt < 16; mt++) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
         float m_run = -INFINITY, l_run = 0.f;
         const float sl2 = p.scale_log2;
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();   // every wave has read its Q rows: buffers 1 may take the second tile
+        // Every wave has read its Q rows (the second tile may take their buffers) and the first
+        // tile has landed. The next item's block entry loads during this wait.
+        if (nxt >= 0)
+            asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier"
+                         : "=s"(ne) : "s"(p.blocks + 8 * (nxt / p.nh)) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (tr) tr[4] = wall_clock64();
         auto zero_tail = [&](int kb, uint16_t *Vs) {   // V^T entries of keys >= k_len -> 0
             const int valid = k_len - kb;
@@ -498,28 +510,34 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         };
-        for (int t = 0; t < n_tiles; t += 2) {
-            tile(t, std::integral_constant<int, 0>{});
-            if (t + 1 < n_tiles) tile(t + 1, std::integral_constant<int, 1>{});
+        if (par == 0) {
+            for (int t = 0; t < n_tiles; t += 2) {
+                tile(t, std::integral_constant<int, 0>{});
+                if (t + 1 < n_tiles) tile(t + 1, std::integral_constant<int, 1>{});
+            }
+        } else {
+            for (int t = 0; t < n_tiles; t += 2) {
+                tile(t, std::integral_constant<int, 1>{});
+                if (t + 1 < n_tiles) tile(t + 1, std::integral_constant<int, 0>{});
+            }
         }
         if (tr) tr[5] = wall_clock64();
 
         // ---- Epilogue: O / l times sigmoid(gate); lane (q16, g) holds dims 32u + 8g + [0, 8).
-        // The gate rows sit in the buffers the last tile left idle (buffers 1 when the tile count
-        // is odd, 0 when even). The next item's loads whose buffers are free already (its first
-        // tile into buffers 0, or its Q rows into buffers 1) are issued before the epilogue, the
-        // other half once every wave has read its gate values.
+        // The gate rows sit in the buffers the last tile left idle. The next item's Q rows and
+        // rotary cos/sin load before the gate work, its Q rows into the buffers the last tile used
+        // (every wave left that tile at its closing barrier); its first tile goes into the gate's
+        // buffers once every wave has read its gate values.
         const float l_row = xrow_sum(l_run);   // outside the row-divergent branch: lanes exchange values
-        const int gate_buf = n_tiles & 1;
+        const int last_buf = (par + n_tiles + 1) & 1;
+        const int gate_buf = last_buf ^ 1;
         const int q_row0 = cur.q_row0, flag_row = cur.flag_row, h = cur.h;
-        item = items.get(k + 1);
+        item = nxt;
         if (item >= 0) {
-            cur = decode(item);
-            if (gate_buf) {
-                if (cur.n_tiles > 0) load_tiles(cur, 0, k0s, v0s);
-            } else {
-                load_rows(cur, k1s, v1s, 0);
-            }
+            cur = decode_from(ne, item);
+            if (last_buf) load_rows(cur, k1s, v1s, 0);
+            else load_rows(cur, k0s, v0s, 0);
+            load_cs(cur);
         }
         if (q_valid) {
             const float il = l_row > 0.f ? 1.f / l_row : 0.f;
@@ -564,11 +582,11 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             // every wave has read its gate values (each read waited for): their buffers are free.
             // A bare barrier: a fence would also wait for the stores and the fills in flight.
             __builtin_amdgcn_s_barrier();
-            if (gate_buf) {
-                load_rows(cur, k1s, v1s, 0);
-            } else {
-                if (cur.n_tiles > 0) load_tiles(cur, 0, k0s, v0s);
+            if (cur.n_tiles > 0) {
+                if (gate_buf) load_tiles(cur, 0, k1s, v1s);
+                else load_tiles(cur, 0, k0s, v0s);
             }
+            par = gate_buf;
         }
         if (tr) tr[1] = wall_clock64();
         if (item < 0) break;
