@@ -18,7 +18,8 @@ BLOCK_INTS = 8
 # Every symbol include/clef_hip_attn.h declares.
 EXPORTS = (
     "clef_hip_attn_version", "clef_hip_attn_wave_size", "clef_hip_attn_init",
-    "clef_hip_attn_plan_max_blocks", "clef_hip_attn_plan",
+    "clef_hip_attn_plan_max_blocks", "clef_hip_attn_plan", "clef_hip_attn_sched_size",
+    "clef_hip_attn_schedule",
     "clef_hip_rope_inv_freq", "clef_hip_vis_positions", "clef_hip_attn_prep_kv",
     "clef_hip_attn_core", "clef_hip_attn_prefill", "clef_hip_vis_attention",
     "clef_hip_record_positions", "clef_hip_pack_batch",
@@ -40,7 +41,7 @@ class AttnArgs(ctypes.Structure):
         ("kv_tok", c_void_p),
         ("kv_rows", c_int), ("causal", c_int), ("gate", c_int),
         ("out", c_void_p), ("out_type", c_int), ("f16_lim", c_float), ("ovf", c_void_p),
-        ("trace", c_void_p),
+        ("trace", c_void_p), ("sched", c_void_p), ("n_wg", c_int),
     ]
 
 
@@ -119,6 +120,11 @@ def load():
                                        POINTER(c_int32), c_int,
                                        POINTER(c_int), POINTER(c_int), c_char_p, c_size_t]
     lib.clef_hip_attn_plan.restype = c_bool
+    lib.clef_hip_attn_sched_size.argtypes = [c_int, c_int, c_int]
+    lib.clef_hip_attn_sched_size.restype = c_int
+    lib.clef_hip_attn_schedule.argtypes = [POINTER(c_int32), c_int, c_int, c_int, c_int, POINTER(c_int32), c_int,
+                                           c_char_p, c_size_t]
+    lib.clef_hip_attn_schedule.restype = c_bool
     lib.clef_hip_rope_inv_freq.argtypes = [c_float, c_int, POINTER(c_float)]
     lib.clef_hip_rope_inv_freq.restype = None
     lib.clef_hip_vis_positions.argtypes = [POINTER(c_int32), c_int, POINTER(c_int32), c_int,

@@ -37,6 +37,16 @@ def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+_CUS = {}
+
+
+def _device_cus(dev):
+    """Compute units of a device (the persistent grid's workgroup count)."""
+    if dev.index not in _CUS:
+        _CUS[dev.index] = torch.cuda.get_device_properties(dev).multi_processor_count
+    return _CUS[dev.index]
+
+
 def _device(device):
     """torch.device with an explicit index for cuda ("cuda" -> "cuda:<current>")."""
     d = torch.device(device)
@@ -132,6 +142,22 @@ class AttnPlan:
         # kv rows the planes must hold, rounded to the 16-byte V^T chunk
         self.kvT = max(8, (self.kv_rows + 7) // 8 * 8)
 
+    def schedule(self, nh, nkv, n_wg):
+        """Per-workgroup item lists of the attention core over n_wg workgroups (device int32,
+        clef_hip_attn_schedule), built once per (nh, nkv, n_wg) and kept with the plan."""
+        key = (nh, nkv, n_wg)
+        cache = self.__dict__.setdefault("_sched", {})
+        if key not in cache:
+            lib = _lib.load()
+            n = lib.clef_hip_attn_sched_size(self.n_blk, nh, n_wg)
+            sched = np.zeros(max(n, 1), dtype=np.int32)
+            blocks = np.ascontiguousarray(self.blocks_host, dtype=np.int32)
+            err = _err()
+            _lib.check(lib.clef_hip_attn_schedule(_i32p(blocks), self.n_blk, nh, nkv, n_wg,
+                                                  _i32p(sched), len(sched), err, len(err)), err)
+            cache[key] = torch.from_numpy(sched).to(self.device)
+        return cache[key]
+
     def pairs(self):
         """(query, key) pairs the plan visits under its mask: the algorithmic work unit."""
         total = 0
@@ -181,7 +207,10 @@ class TextAttention:
         return torch.empty((max(T, 1), max(self.n_rot // 2, 1), 2), dtype=torch.float32, device=self.device)
 
     def args(self, qkv, q_norm, k_norm, pos3, plan, out, k_plane, vt_plane, kvT,
-             out_type=OUT_BF16, gate=True, ovf=None, f16_lim=65504.0, rope_cs=None, trace=None):
+             out_type=OUT_BF16, gate=True, ovf=None, f16_lim=65504.0, rope_cs=None, trace=None,
+             schedule=True):
+        """The C argument block. schedule: hand the core a per-workgroup item split over the
+        device's CUs (clef_hip_attn_schedule), else it falls back to its static order."""
         T = plan.T
         dev = self.device
         _check(qkv, "qkv", (T, qkv.shape[1] if qkv.dim() == 2 else -1), torch.bfloat16, dev)
@@ -222,11 +251,14 @@ class TextAttention:
         a.causal, a.gate = int(plan.causal), int(gate)
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
         a.trace = _ptr(trace)
+        if schedule and plan.n_blk:
+            n_wg = _device_cus(dev)
+            a.sched, a.n_wg = _ptr(plan.schedule(self.nh, self.nkv, n_wg)), n_wg
         return a
 
     def forward(self, qkv, q_norm, k_norm, pos3, plan, out=None, out_dtype="bf16", gate=True,
                 k_plane=None, vt_plane=None, kvT=None, ovf=None, f16_lim=65504.0, stream=None,
-                stage="prefill", rope_cs=None, trace=None):
+                stage="prefill", rope_cs=None, trace=None, schedule=True):
         """Runs one layer's attention. stage: "prefill" (prep_kv + core), "prep", or "core".
         rope_cs: the rotary cos/sin scratch (see rope_table); allocated here for "prefill" when
         not given. A "core" call with a table reads what the last "prep" call wrote."""
@@ -243,7 +275,7 @@ class TextAttention:
             rope_cs = self.rope_table(plan.T)
         a = self.args(qkv, q_norm, k_norm, pos3, plan, out, k_plane, vt_plane, kvT,
                       out_type=out_type, gate=gate, ovf=ovf, f16_lim=f16_lim, rope_cs=rope_cs,
-                      trace=trace)
+                      trace=trace, schedule=schedule)
         fn = {"prefill": lib.clef_hip_attn_prefill, "prep": lib.clef_hip_attn_prep_kv,
               "core": lib.clef_hip_attn_core}[stage]
         err = _err()

@@ -120,6 +120,50 @@ bool clef_hip_attn_init(char *err, size_t errlen) {
     return true;
 }
 
+int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg) {
+    if (n_blk < 0 || nh <= 0 || n_wg <= 0) return 0;
+    return n_wg + 1 + n_blk * nh;
+}
+
+bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,
+                            int32_t *sched, int max_sched, char *err, size_t errlen) {
+    if ((n_blk && !blocks) || !sched || n_blk < 0 || nh <= 0 || nkv <= 0 || nh % nkv || n_wg <= 0)
+        return fail(err, errlen, "bad schedule arguments");
+    const long need = (long)n_wg + 1 + (long)n_blk * nh;
+    if (need > max_sched) return fail(err, errlen, "schedule needs %ld entries, room for %d", need, max_sched);
+    // cost of an item in 64-key tiles: its tiles plus the prologue / epilogue (Q rows, gate,
+    // output stores), measured at about three tiles' time per item
+    constexpr int kFixed = 3;
+    const int xh = (nh % 8 == 0 && ((nh / nkv) % (nh / 8) == 0 || (nh / 8) % (nh / nkv) == 0)) ? nh / 8 : 0;
+    const int groups = (xh && n_wg % 8 == 0) ? 8 : 1;
+    std::vector<std::vector<int>> lists(n_wg);
+    std::vector<long> load(n_wg, 0);
+    for (int x = 0; x < groups; x++) {
+        // items of this XCD group, longest first (the plan's blocks already are)
+        std::vector<std::pair<int, int>> its;   // (cost, item)
+        for (int bi = 0; bi < n_blk; bi++) {
+            const int cost = (blocks[8 * bi + 4] + 63) / 64 + kFixed;
+            for (int h = 0; h < nh; h++)
+                if (groups == 1 || h / xh == x) its.push_back({cost, bi * nh + h});
+        }
+        std::stable_sort(its.begin(), its.end(), [](const std::pair<int, int> &u, const std::pair<int, int> &v) { return u.first > v.first; });
+        for (const auto &it : its) {
+            int best = -1;
+            for (int b = x; b < n_wg; b += groups)
+                if (best < 0 || load[b] < load[best]) best = b;
+            load[best] += it.first;
+            lists[best].push_back(it.second);
+        }
+    }
+    int off = 0;
+    for (int b = 0; b < n_wg; b++) {
+        sched[b] = off;
+        for (int it : lists[b]) sched[n_wg + 1 + off++] = it;
+    }
+    sched[n_wg] = off;
+    return true;
+}
+
 int clef_hip_attn_plan_max_blocks(int n_seq, int Tq) {
     if (n_seq < 0 || Tq < 0) return 0;
     return Tq / CLEF_HIP_BLOCK_Q + n_seq + 1;
@@ -249,7 +293,11 @@ bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, si
     const long n_items = (long)a->n_blk * a->nh;
     if (n_items > 0x7fffffffL) return fail(err, errlen, "grid too large");
     long grid = n_items;
-    if (text_persistent()) {
+    if (a->sched) {
+        if (a->n_wg <= 0) return fail(err, errlen, "bad n_wg %d for the schedule", a->n_wg);
+        p.sched = a->sched;
+        grid = a->n_wg;
+    } else if (text_persistent()) {
         // one workgroup per CU, each looping over its items (a multiple of 8 for the XCD mapping)
         const long cus = device_cus();
         if (cus > 0 && cus < n_items) grid = p.xcd_heads ? std::max(8L, cus / 8 * 8) : cus;

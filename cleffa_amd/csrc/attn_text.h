@@ -97,24 +97,41 @@ __device__ __forceinline__ void static_for(F &&f) {
 }
 }  // namespace text
 
-// Work items are (query block, q head) pairs. Workgroup b takes items get(0), get(1), ... from a
-// static list. With xcd_heads, the items of XCD x (workgroup ids go round-robin over the 8 XCDs,
-// each with its own L2) are the heads x*xcd_heads .. +xcd_heads-1 of every block, so an XCD
-// streams the K/V of as few kv heads as possible; items keep the plan's longest-first block
-// order and are dealt to the XCD's workgroups in snake order (round r left to right when r is
-// even, right to left when odd), so long and short blocks mix. A grid of one workgroup per item
-// gives every workgroup exactly one.
+// Work items are (query block, q head) pairs. Workgroup b takes items get(0), get(1), ... With a
+// host schedule (p.sched, clef_hip_attn_schedule) they are the workgroup's own list. Otherwise
+// they come from a static order: with xcd_heads, the items of XCD x (workgroup ids go round-robin
+// over the 8 XCDs, each with its own L2) are the heads x*xcd_heads .. +xcd_heads-1 of every block,
+// so an XCD streams the K/V of as few kv heads as possible; items keep the plan's longest-first
+// block order and are dealt to the XCD's workgroups in snake order (round r left to right when r
+// is even, right to left when odd), so long and short blocks mix. A grid of one workgroup per
+// item gives every workgroup exactly one.
+// Schedule entries are read with scalar loads, which leave the vector memory counter (the tile
+// fills' waits count on it) alone.
+__device__ __forceinline__ int sload(const int32_t *ptr) {
+    int v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(ptr) : "memory");
+    return v;
+}
 struct ItemList {
-    int n_items, per_x, gx, xh, nh;
+    int n_items, per_x, gx, xh, nh, s0, s1;
+    const int32_t *list;
     __device__ __forceinline__ void setup(const AttnParams &p) {
         nh = p.nh;
         xh = p.xcd_heads;
         gx = (int)gridDim.x >> 3;
         n_items = p.n_blk * p.nh;
         per_x = xh ? p.n_blk * xh : 0;
+        list = nullptr;
+        s0 = s1 = 0;
+        if (p.sched) {
+            s0 = sload(p.sched + blockIdx.x);
+            s1 = sload(p.sched + blockIdx.x + 1);
+            list = p.sched + gridDim.x + 1;
+        }
     }
     // the k-th item of this workgroup as block * nh + head, or -1
     __device__ __forceinline__ int get(int k) const {
+        if (list) return s0 + k < s1 ? sload(list + s0 + k) : -1;
         if (xh && gx && ((int)gridDim.x & 7) == 0) {
             const int x = blockIdx.x & 7, wl = blockIdx.x >> 3;
             const int j = k * gx + ((k & 1) ? gx - 1 - wl : wl);

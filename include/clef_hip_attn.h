@@ -117,7 +117,24 @@ typedef struct {
                                  registers, end of the prologue, end of the key loop, workgroup,
                                  ordinal in the workgroup; the CLEF_PROFILE analogue
                                  (clef_metal.m:52-68) at work-item grain */
+    const int32_t *sched;     /* NULL, or device copy of clef_hip_attn_schedule's output for this
+                                 plan, nh and n_wg: the core then runs n_wg workgroups, each
+                                 over its own item list */
+    int n_wg;
 } clef_hip_attn_args;
+
+/* Static split of a text pass's work items (query block, q head) over n_wg workgroups of the
+ * attention core, for clef_hip_attn_args.sched. No reference counterpart: the Metal backend
+ * dispatches one threadgroup per block and head (clef_metal.m:829-882); a persistent grid needs
+ * the split made on the host. Items are dealt longest first to the least loaded workgroup
+ * (cost: the block's 64-key tiles plus a fixed per-item cost), within the workgroups of the XCD
+ * that owns the item's q head when the heads divide evenly over the 8 XCDs (workgroup b runs on
+ * XCD b % 8). blocks: the plan's host block list. Output: sched[0..n_wg] item offsets per
+ * workgroup, then the items as block * nh + head, each workgroup's longest first;
+ * clef_hip_attn_sched_size gives the entry count. */
+int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg);
+bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,
+                            int32_t *sched, int max_sched, char *err, size_t errlen);
 
 /* K/V prologue only: RMSNorm + rotary of each pass row's K into its plane row (kv_tok), V into
  * the V^T plane (attn_prep / attn_prep_split / attn_prep_prefix K and V parts,

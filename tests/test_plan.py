@@ -84,3 +84,59 @@ def test_pairs_counts_causal_and_bidirectional():
     cu = np.array([0, 3, 10], np.int32)
     assert AttnPlan(cu, device="cpu").pairs() == 6 + 28
     assert AttnPlan(cu, causal=False, device="cpu").pairs() == 9 + 49
+
+
+def _sched(plan, nh, nkv, n_wg):
+    import ctypes
+    from cleffa_amd import _lib
+    lib = _lib.load()
+    n = lib.clef_hip_attn_sched_size(plan.n_blk, nh, n_wg)
+    out = np.zeros(max(n, 1), np.int32)
+    err = ctypes.create_string_buffer(256)
+    b = np.ascontiguousarray(plan.blocks_host, dtype=np.int32)
+    p = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    ok = lib.clef_hip_attn_schedule(p(b), plan.n_blk, nh, nkv, n_wg, p(out), len(out), err, len(err))
+    return ok, out, err.value.decode()
+
+
+@pytest.mark.parametrize("lengths,nh,nkv,n_wg", [
+    ([1160, 890, 730, 425, 472, 136, 179, 104], 24, 4, 256),   # C1: heads split over the 8 XCDs
+    ([16384], 24, 4, 256),
+    ([512] * 4, 16, 4, 256),
+    ([300, 17, 1], 12, 4, 7),                                    # no XCD split
+    ([5], 2, 1, 300),                                            # more workgroups than items
+])
+def test_schedule_covers_items_balanced(lengths, nh, nkv, n_wg):
+    """clef_hip_attn_schedule: every (block, head) item exactly once, each workgroup's items
+    longest first, items of an XCD's heads only on that XCD's workgroups, and greedy balance
+    (no workgroup above the mean load by more than one item's cost)."""
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    plan = AttnPlan(cu, causal=True, device="cpu")
+    ok, s, err = _sched(plan, nh, nkv, n_wg)
+    assert ok, err
+    off, items = s[: n_wg + 1], s[n_wg + 1:]
+    assert off[0] == 0 and (np.diff(off) >= 0).all() and off[-1] == plan.n_blk * nh
+    assert sorted(items.tolist()) == list(range(plan.n_blk * nh))
+    cost = lambda it: (int(plan.blocks_host[it // nh][4]) + 63) // 64 + 3
+    xh = nh // 8 if nh % 8 == 0 and ((nh // nkv) % (nh // 8) == 0 or (nh // 8) % (nh // nkv) == 0) else 0
+    split = xh and n_wg % 8 == 0
+    loads = []
+    for b in range(n_wg):
+        mine = items[off[b]:off[b + 1]].tolist()
+        c = [cost(it) for it in mine]
+        assert c == sorted(c, reverse=True)
+        if split:
+            assert all((it % nh) // xh == b % 8 for it in mine)
+        loads.append(sum(c))
+    groups = 8 if split else 1
+    for x in range(groups):
+        ld = loads[x::groups]
+        tot = sum(cost(it) for it in items.tolist() if not split or (it % nh) // xh == x)
+        biggest = max([cost(it) for it in items.tolist() if not split or (it % nh) // xh == x], default=0)
+        assert max(ld) <= tot / len(ld) + biggest
+
+
+def test_schedule_errors():
+    plan = AttnPlan(np.array([0, 100], np.int32), causal=True, device="cpu")
+    ok, _, err = _sched(plan, 6, 4, 8)       # nh not a multiple of nkv
+    assert not ok and "bad schedule" in err
