@@ -8,7 +8,7 @@ REPO = ROOT.parent
 LIB = ROOT / "libclef_hip_attn.so"
 SOURCES = [ROOT / "csrc" / "attn_api.hip", ROOT / "csrc" / "prefix_cache.hip", ROOT / "csrc" / "omni_api.hip", ROOT / "csrc" / "records.cpp",
            ROOT / "csrc" / "gemm_api.cpp"]
-DEPS = SOURCES + [ROOT / "csrc" / "attn_kernels.h", ROOT / "csrc" / "attn_params.h", ROOT / "csrc" / "attn_text.h", ROOT / "csrc" / "attn_text_pair.h",
+DEPS = SOURCES + [ROOT / "csrc" / "attn_kernels.h", ROOT / "csrc" / "attn_params.h", ROOT / "csrc" / "attn_text.h",
                   ROOT / "csrc" / "attn_vis.h", ROOT / "csrc" / "omni_attn.h",
                   REPO / "include" / "clef_hip_attn.h"]
 

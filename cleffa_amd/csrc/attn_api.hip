@@ -11,7 +11,6 @@
 
 #include "attn_kernels.h"
 #include "attn_text.h"
-#include "attn_text_pair.h"
 #include "attn_vis.h"
 #include "attn_params.h"
 #include "clef_hip_attn.h"
@@ -85,13 +84,6 @@ bool text_persistent() {
     return !(e && e[0] == '0');
 }
 
-// Text kernel form: one wave per 16 query rows (default), or wave pairs sharing 32 rows with
-// CLEF_HIP_TEXT_KERNEL=pair.
-bool text_pair() {
-    const char *e = getenv("CLEF_HIP_TEXT_KERNEL");
-    return e && !strcmp(e, "pair");
-}
-
 long device_cus() {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
@@ -115,7 +107,7 @@ bool clef_hip_attn_init(char *err, size_t errlen) {
     if (e != hipSuccess) return fail(err, errlen, "device query failed: %s", hipGetErrorString(e));
     if (!strstr(prop.gcnArchName, "gfx950")) return fail(err, errlen, "kernels are built for gfx950, device is %s", prop.gcnArchName);
     if (prop.warpSize != 64) return fail(err, errlen, "attention kernels need 64-wide wavefronts (device reports %d)", prop.warpSize);
-    const size_t need = tpair::SMEM_BYTES + sizeof(float) * text::HD;
+    const size_t need = sizeof(uint16_t) * text::LDS_ELEMS;
     if (prop.sharedMemPerBlock < need) return fail(err, errlen, "device LDS %zu < %zu bytes", (size_t)prop.sharedMemPerBlock, need);
     return true;
 }
@@ -302,14 +294,10 @@ bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, si
         const long cus = device_cus();
         if (cus > 0 && cus < n_items) grid = p.xcd_heads ? std::max(8L, cus / 8 * 8) : cus;
     }
-    const bool pair = text_pair();
-    if (a->n_rot == 64) {
-        if (pair) hipLaunchKernelGGL(attn_text_pair_kernel<64>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);
-        else hipLaunchKernelGGL(attn_text_kernel<64>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);
-    } else {
-        if (pair) hipLaunchKernelGGL(attn_text_pair_kernel<0>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);
-        else hipLaunchKernelGGL(attn_text_kernel<0>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);
-    }
+    if (a->n_rot == 64)
+        hipLaunchKernelGGL(attn_text_kernel<64>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);
+    else
+        hipLaunchKernelGGL(attn_text_kernel<0>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);
     return launch_ok("attn_fwd<256>", err, errlen);
 }
 
