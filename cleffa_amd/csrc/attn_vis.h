@@ -8,7 +8,12 @@
 // workgroups per CU.
 // The 72-dim contraction runs as three 32-dim chunks: Q holds zeros in dims 72..95, and the
 // K slots of those dims hold copies of real K chunks of the same row (finite), so they add 0.
-// O^T covers 96 rows: V^T rows 72..95 of both LDS buffers are zeroed once per workgroup.
+// O^T covers 96 rows: V^T rows 73..95 of both LDS buffers are zeroed once per workgroup and row
+// 72 is set to 1, so O^T row 72 accumulates the row sum of the rounded P (the softmax
+// denominator, rescaled with O) in the padding products the MFMAs run anyway.
+// Q is pre-scaled by scale * log2 e and the S accumulators start at minus the row's running max,
+// so the products deliver the exponent of P directly; only when a tile moves the max (by more
+// than 8, rarely) is the difference subtracted and O rescaled.
 #pragma once
 #include "attn_text.h"
 
@@ -122,10 +127,12 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
     const unsigned va1 = vl + 2 * (vrow * BK + (((4 + g) ^ vx) * 8));
 
     const int n_tiles = (k_len + BK - 1) / BK;
-    // V^T rows 72..95 of both buffers stay zero
+    // V^T rows 72..95 of both buffers: row 72 all ones (bf16 1.0), the rest zero. A row is 64
+    // keys in 8 chunks whose order the swizzle permutes; the values are the same in every chunk.
     for (int i = tid; i < 2 * (HDV - HD) * BK / 8; i += 256) {
         const int b = i / ((HDV - HD) * BK / 8), r = i % ((HDV - HD) * BK / 8);
-        *(u32x4 *)((b ? v1s : v0s) + HD * BK + r * 8) = u32x4{0, 0, 0, 0};
+        const unsigned one = r < BK / 8 ? 0x3f803f80u : 0u;
+        *(u32x4 *)((b ? v1s : v0s) + HD * BK + r * 8) = u32x4{one, one, one, one};
     }
     if (n_tiles > 0) load_tiles(0, k0s, v0s);
 
@@ -141,7 +148,10 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
         for (int c = 0; c < NC; c++) {
             const int ch = 4 * c + g;
             const u32x4 w = (q_valid && ch < RCH) ? *(const u32x4 *)(src + ch * 8) : u32x4{0, 0, 0, 0};
-            qf[hh][c] = __builtin_bit_cast(bf16x8, w);
+            u32x4 ws;
+#pragma unroll
+            for (int j = 0; j < 4; j++) ws[j] = pack_bf16(bf_lo(w[j]) * p.scale_log2, bf_hi(w[j]) * p.scale_log2);
+            qf[hh][c] = __builtin_bit_cast(bf16x8, ws);
         }
     }
     f32x4 o[2][NM];
@@ -149,8 +159,8 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
     for (int hh = 0; hh < 2; hh++)
 #pragma unroll
         for (int mt = 0; mt < NM; mt++) o[hh][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
-    const float sl2 = p.scale_log2;
+    // running max per half in the scaled (log2) domain; msub: what the S accumulators start from
+    float m_run[2] = {-INFINITY, -INFINITY};
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -171,12 +181,17 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
                 constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
                 ring[st] = lds_read16<buf * 2 * KTILE>(ka[kt][c]);
             });
+            const float ms0 = m_run[0] == -INFINITY ? 0.f : m_run[0];
+            const float ms1 = m_run[1] == -INFINITY ? 0.f : m_run[1];
             static_for<QK>([&](auto I) {   // one K operand, both halves' products
                 constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
                 constexpr int ahead = (QK - 1 - st) < (DEPTH - 1) ? (QK - 1 - st) : (DEPTH - 1);
                 bf16x8 a = ring[st % DEPTH];
                 lds_wait<ahead>(a);
-                if constexpr (c == 0) s[0][kt] = s[1][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if constexpr (c == 0) {
+                    s[0][kt] = f32x4{-ms0, -ms0, -ms0, -ms0};
+                    s[1][kt] = f32x4{-ms1, -ms1, -ms1, -ms1};
+                }
                 s[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][c], s[0][kt], 0, 0, 0);
                 s[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][c], s[1][kt], 0, 0, 0);
                 if constexpr (st + DEPTH < QK) {
@@ -207,40 +222,32 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
                 float mx = -INFINITY;
 #pragma unroll
                 for (int kt = 0; kt < 4; kt++)
+                    mx = fmaxf(fmaxf(mx, fmaxf(s[hh][kt][0], s[hh][kt][1])), fmaxf(s[hh][kt][2], s[hh][kt][3]));
+                // s holds score - running max. The max moves only when a tile's max passes it by
+                // more than 8 (log2 units), or on the first tile: P stays below 2^8, and the
+                // shift and the O rescale below run on few tiles. The lane's own max decides
+                // whether any row may move; only then is the row max reduced over its four lanes.
+                const float mr = m_run[hh];
+                if (__any(mx > 8.f || mr == -INFINITY)) {
+                    const float rmx = xrow_max(mx);
+                    const float d = (mr == -INFINITY || rmx > 8.f) ? (rmx == -INFINITY ? 0.f : rmx) : 0.f;
+                    const float alpha = (mr == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(-d);
+                    m_run[hh] = (mr == -INFINITY) ? (rmx == -INFINITY ? -INFINITY : d) : mr + d;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[hh][kt][i]);
-                // The running max moves only when a tile's max passes it by more than 8 (log2
-                // units): P stays below 2^8, and the O rescale below runs on few tiles. The
-                // lane's own max decides whether any row may move; only then is the row max
-                // reduced over the row's four lanes.
-                float mn = m_run[hh];
-                if (__any(mx * sl2 > m_run[hh] + 8.f)) {
-                    const float rmx = xrow_max(mx) * sl2;
-                    mn = (rmx > m_run[hh] + 8.f) ? rmx : m_run[hh];
+                    for (int kt = 0; kt < 4; kt++) s[hh][kt] -= d;
+#pragma unroll
+                    for (int mt = 0; mt < NM; mt++) o[hh][mt] *= alpha;
                 }
-                const float msub = (mn == -INFINITY) ? 0.f : mn;
-                const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run[hh] - mn);
-                float rs = 0.f;
 #pragma unroll
                 for (int kc = 0; kc < 2; kc++) {
                     unsigned w[4];
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const int kt = 2 * kc + (j >> 1), i = 2 * (j & 1);
-                        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[hh][kt][i], sl2, -msub));
-                        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[hh][kt][i + 1], sl2, -msub));
-                        w[j] = pack_bf16(p0, p1);
-                        rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]),
-                                                             bf16x2{(__bf16)1.0f, (__bf16)1.0f}, rs, false);
+                        w[j] = pack_bf16(__builtin_amdgcn_exp2f(s[hh][kt][i]), __builtin_amdgcn_exp2f(s[hh][kt][i + 1]));
                     }
                     u32x4 wv = {w[0], w[1], w[2], w[3]};
                     pk[hh][kc] = __builtin_bit_cast(bf16x8, wv);
-                }
-                l_run[hh] = l_run[hh] * alpha + rs;   // the lane's share, rows added up at the end
-                m_run[hh] = mn;
-                if (__any(alpha != 1.f)) {
-#pragma unroll
-                    for (int mt = 0; mt < NM; mt++) o[hh][mt] *= alpha;
                 }
             }
             static_for<PV>([&](auto I) {   // one V^T operand, both halves' products
@@ -266,7 +273,8 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
         const int my_q = wave * ROWS + 16 * hh + q16;
-        const float l_row = xrow_sum(l_run[hh]);   // before the row-divergent exit: lanes exchange values
+        // the row sum sits in O^T row 72: tile 4, lane 16 + q16, element 0
+        const float l_row = __shfl(o[hh][4][0], 16 + q16);   // before the row-divergent exit
         if (my_q >= nq) continue;
         const float il = l_row > 0.f ? 1.f / l_row : 0.f;
         const size_t t = (size_t)q_row0 + my_q;
