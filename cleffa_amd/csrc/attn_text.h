@@ -387,8 +387,11 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             }
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                u32x4 w = {pack_f16(x[c][0], x[c][1]), pack_f16(x[c][2], x[c][3]),
-                           pack_f16(x[c][4], x[c][5]), pack_f16(x[c][6], x[c][7])};
+                // scaled by scale * log2 e before the one rounding to f16: the products give
+                // scores in the exp2 domain
+                const float sc = p.scale_log2;
+                u32x4 w = {pack_f16(x[c][0] * sc, x[c][1] * sc), pack_f16(x[c][2] * sc, x[c][3] * sc),
+                           pack_f16(x[c][4] * sc, x[c][5] * sc), pack_f16(x[c][6] * sc, x[c][7] * sc)};
                 qf[c] = __builtin_bit_cast(f16x8, w);
             }
         }
@@ -396,8 +399,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         f32x4 o[16];
 #pragma unroll
         for (int mt = 0; mt < 16; mt++) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        float m_run = -INFINITY, l_run = 0.f;
-        const float sl2 = p.scale_log2;
+        float m_run = -INFINITY, l_run = 0.f, msub = 0.f;   // msub: where the S accumulators start (-msub)
         // Every wave has read its Q rows (the second tile may take their buffers) and the first
         // tile has landed. The next item's block entry loads during this wait.
         if (nxt >= 0)
@@ -449,7 +451,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                     constexpr int ahead = (QK - 1 - st) < (DEPTH - 1) ? (QK - 1 - st) : (DEPTH - 1);
                     bf16x8 a = ring[st % DEPTH];
                     lds_wait<ahead>(a);
-                    if constexpr (c == 0) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (c == 0) s[kt] = f32x4{-msub, -msub, -msub, -msub};
                     s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), qf[c], s[kt], 0, 0, 0);
                     if constexpr (st + DEPTH < QK) {
                         constexpr int n = st + DEPTH, nkt = n & 3, nc = n >> 2;
@@ -475,22 +477,25 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                         for (int i = 0; i < 4; i++)
                             s[kt][i] = (32 * (kt >> 1) + 4 * (kt & 1) + i > lim) ? -INFINITY : s[kt][i];
                 }
+                // s holds the score minus the running max (exp2 domain). The max moves only when a
+                // tile's max passes it by more than 8, or on the row's first tile: P stays below
+                // 2^8, and the shift and the O rescale below run on few tiles. The lane's own max
+                // decides whether any row of the wave may move; only then is the row max reduced
+                // over the row's four lanes.
                 float mx = -INFINITY;
 #pragma unroll
                 for (int kt = 0; kt < 4; kt++)
+                    mx = fmaxf(fmaxf(mx, fmaxf(s[kt][0], s[kt][1])), fmaxf(s[kt][2], s[kt][3]));
+                float alpha = 1.f;
+                if (__any(mx > 8.f || m_run == -INFINITY)) {
+                    const float rmx = xrow_max(mx);
+                    const float d = (m_run == -INFINITY || rmx > 8.f) ? (rmx == -INFINITY ? 0.f : rmx) : 0.f;
+                    alpha = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(-d);
+                    m_run = (m_run == -INFINITY) ? (rmx == -INFINITY ? -INFINITY : d) : m_run + d;
+                    msub = m_run == -INFINITY ? 0.f : m_run;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kt][i]);
-                // The running max moves only when a tile's max passes it by more than 8 (log2
-                // units): P stays below 2^8, and the O rescale below runs on few tiles. The lane's
-                // own max decides whether any row of the wave may move; only then is the row max
-                // reduced over the row's four lanes.
-                float mn = m_run;
-                if (__any(mx * sl2 > m_run + 8.f)) {
-                    const float rmx = xrow_max(mx) * sl2;
-                    mn = (rmx > m_run + 8.f) ? rmx : m_run;
+                    for (int kt = 0; kt < 4; kt++) s[kt] -= d;
                 }
-                const float msub = (mn == -INFINITY) ? 0.f : mn;
-                const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
                 float rs = 0.f;
                 bf16x8 pk[2];
 #pragma unroll
@@ -499,9 +504,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const int kt = 2 * kc + (j >> 1), i = 2 * (j & 1);
-                        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][i], sl2, -msub));
-                        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][i + 1], sl2, -msub));
-                        w[j] = pack_bf16(p0, p1);
+                        w[j] = pack_bf16(__builtin_amdgcn_exp2f(s[kt][i]), __builtin_amdgcn_exp2f(s[kt][i + 1]));
                         // the row sum takes the rounded P that the PV product multiplies
                         rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[j]),
                                                              bf16x2{(__bf16)1.0f, (__bf16)1.0f}, rs, false);
@@ -510,7 +513,6 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                     pk[kc] = __builtin_bit_cast(bf16x8, wv);
                 }
                 l_run = l_run * alpha + rs;   // the lane's share; the row's four lanes add up at the end
-                m_run = mn;
                 if (__any(alpha != 1.f)) {
 #pragma unroll
                     for (int mt = 0; mt < 16; mt++) o[mt] *= alpha;
