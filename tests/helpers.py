@@ -28,12 +28,14 @@ def oracle_text(w, rows=None, precision="f64", gate=None, causal=True):
                             rows=rows, precision=precision)
 
 
-def gpu_text(w, out_dtype="bf16", gate=None, causal=True, ovf=None, device="cuda", f16_lim=65504.0):
+def gpu_text(w, out_dtype="bf16", gate=None, causal=True, ovf=None, device="cuda", f16_lim=65504.0,
+             schedule=True):
     att = TextAttention(w["nh"], w["nkv"], w["hd"], w["n_rot"], rope_theta=w.get("theta", 1e7), device=device)
     plan = AttnPlan(w["cu_seqlens"], causal=causal, device=device)
     d = lambda t: None if t is None else t.to(device)
     out = att.forward(d(w["qkv"]), d(w["q_norm"]), d(w["k_norm"]), d(w["pos3"]), plan, out_dtype=out_dtype,
-                      gate=w.get("gate", True) if gate is None else gate, ovf=ovf, f16_lim=f16_lim)
+                      gate=w.get("gate", True) if gate is None else gate, ovf=ovf, f16_lim=f16_lim,
+                      schedule=schedule)
     torch.cuda.synchronize()
     return out, plan
 

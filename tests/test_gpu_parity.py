@@ -259,15 +259,18 @@ def test_vision_mixed_images_and_f16():
     (4, 1, [40, 3]),                                       # fewer items than CUs
 ])
 def test_persistent_grid_matches_one_item_per_workgroup(nh, nkv, lengths, monkeypatch):
-    """The persistent grid (one workgroup per CU looping over its items) and one workgroup per
-    item give the same bytes: each item's arithmetic does not depend on where it runs."""
+    """The host schedule (clef_hip_attn_schedule over the CUs), the persistent grid's static
+    order and one workgroup per item give the same bytes: each item's arithmetic does not depend
+    on where or in which order it runs."""
     _say(f"[invariance] persistent grid nh={nh} nkv={nkv} lengths={lengths}")
     w = workloads.text_inputs(lengths, nh, nkv, seed=31)
     w.update(gate=True, theta=1e7)
+    a, _ = gpu_text(w)                                   # host schedule
     monkeypatch.setenv("CLEF_HIP_TEXT_PERSISTENT", "1")
-    a, _ = gpu_text(w)
+    b, _ = gpu_text(w, schedule=False)                   # persistent grid, static order
     monkeypatch.setenv("CLEF_HIP_TEXT_PERSISTENT", "0")
-    b, _ = gpu_text(w)
+    c, _ = gpu_text(w, schedule=False)                   # one workgroup per item
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(a.view(torch.int16), c.view(torch.int16))
     if sum(lengths) <= 1500:
         assert_close(a.float().cpu().numpy(), oracle_text(w), what="persistent grid")
