@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="C1", choices=["C0", "C1", "C2", "C3", "C4", "P", "O", "G"],
+    ap.add_argument("--config", default="C1", choices=["C0", "C1", "C2", "C3", "C4", "P", "O", "G", "M"],
                     help="C0-C4: attention configurations; P: prefix-cache growth copy (HBM-bound); "
                          "O: Omni attention (hd 128, FP32, 16,344 tokens); G: the QKV and o_proj GEMMs around C1")
     ap.add_argument("--seed", type=int, default=0)
@@ -281,6 +281,37 @@ def bench_gemms(a):
     }), flush=True)
 
 
+def mfma_ceiling(random, iters=4000):
+    """(TF/s, GHz) of clef_hip_mfma_ceiling: the attention kernels' MFMA operand stream with
+    random or constant-pattern bf16 operands, and the shader clock it held."""
+    import ctypes
+    from cleffa_amd import _lib
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    scratch = torch.empty(cus * (2048 + 16), dtype=torch.uint8, device="cuda")
+    tf, ghz = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    err = ctypes.create_string_buffer(256)
+    torch.cuda.synchronize()
+    _lib.check(lib.clef_hip_mfma_ceiling(int(random), iters, scratch.data_ptr(), scratch.numel(),
+                                         ctypes.byref(tf), ctypes.byref(ghz), err, len(err)), err)
+    return tf.value, ghz.value
+
+
+def bench_mfma_ceiling(a):
+    c_tf, c_ghz = mfma_ceiling(False)   # constant operands first, on the cooler part
+    r_tf, r_ghz = mfma_ceiling(True)
+    print(json.dumps({
+        "metric": "MFMA ceiling of the attention operand stream (v_mfma_f32_16x16x32_bf16, one "
+                  "ds_read_b128 A operand per product, 8 waves per CU)",
+        "value": round(r_tf, 1), "unit": "TFLOP/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic: random bf16 operands (the value) and a constant bit pattern",
+        "config": {"workload": "MFMA ceiling, random and constant operands"},
+        "random": {"tflops": round(r_tf, 1), "clock_ghz": round(r_ghz, 3), "frac": round(r_tf / PEAK_BF16_TFLOPS, 4)},
+        "constant": {"tflops": round(c_tf, 1), "clock_ghz": round(c_ghz, 3), "frac": round(c_tf / PEAK_BF16_TFLOPS, 4)},
+        "vs_baseline": None,
+    }), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -297,6 +328,8 @@ def main():
         return bench_omni(a)
     if a.config == "G":
         return bench_gemms(a)
+    if a.config == "M":
+        return bench_mfma_ceiling(a)
     step, core, info, w = build_step(a.config, a.seed)
     if a.profile_pass:
         src = torch.randn(CALIB_BYTES // 2, device="cuda").to(torch.bfloat16)
@@ -336,6 +369,11 @@ def main():
                            "launch_ms": round(core_ms, 5),
                            "algorithmic_bytes": info["bytes"],
                            "hbm_frac_at_this_time": round(info["bytes"] / (core_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        # the same MFMA operand stream with random operands, measured now on this device: the
+        # rate the part's power and clock allow (the nominal peak assumes 2.4 GHz)
+        ceil_tf, ceil_ghz = mfma_ceiling(True)
+        res["roofline"].update({"mfma_stream_ceiling": round(ceil_tf, 1), "mfma_stream_clock_ghz": round(ceil_ghz, 3),
+                                "frac_of_stream_ceiling": round(achieved / ceil_tf, 4)})
         res["prep_ms"] = round(ms - core_ms, 5)
     if not a.no_cpu and a.config in ("C1", "C2") and a.config == "C1":
         sec, threads = cpu_baseline(w, a.config)

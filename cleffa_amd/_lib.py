@@ -19,7 +19,7 @@ BLOCK_INTS = 8
 EXPORTS = (
     "clef_hip_attn_version", "clef_hip_attn_wave_size", "clef_hip_attn_init",
     "clef_hip_attn_plan_max_blocks", "clef_hip_attn_plan", "clef_hip_attn_sched_size",
-    "clef_hip_attn_schedule",
+    "clef_hip_attn_schedule", "clef_hip_mfma_ceiling",
     "clef_hip_rope_inv_freq", "clef_hip_vis_positions", "clef_hip_attn_prep_kv",
     "clef_hip_attn_core", "clef_hip_attn_prefill", "clef_hip_vis_attention",
     "clef_hip_record_positions", "clef_hip_pack_batch",
@@ -120,6 +120,9 @@ def load():
                                        POINTER(c_int32), c_int,
                                        POINTER(c_int), POINTER(c_int), c_char_p, c_size_t]
     lib.clef_hip_attn_plan.restype = c_bool
+    lib.clef_hip_mfma_ceiling.argtypes = [c_int, c_int, c_void_p, c_size_t, POINTER(ctypes.c_double),
+                                          POINTER(ctypes.c_double), c_char_p, c_size_t]
+    lib.clef_hip_mfma_ceiling.restype = c_bool
     lib.clef_hip_attn_sched_size.argtypes = [c_int, c_int, c_int]
     lib.clef_hip_attn_sched_size.restype = c_int
     lib.clef_hip_attn_schedule.argtypes = [POINTER(c_int32), c_int, c_int, c_int, c_int, POINTER(c_int32), c_int,

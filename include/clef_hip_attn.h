@@ -133,6 +133,14 @@ typedef struct {
  * workgroup, then the items as block * nh + head, each workgroup's longest first;
  * clef_hip_attn_sched_size gives the entry count. */
 int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg);
+
+/* Measurement utility, no reference counterpart: the MFMA rate the attention kernels' operand
+ * stream sustains on this device (v_mfma_f32_16x16x32_bf16, one ds_read_b128 A operand per
+ * product, 8 waves per CU), with random (random != 0) or constant-pattern bf16 operands, and the
+ * shader clock it held (cycle counter against the 100 MHz wall clock). Runs on the default
+ * stream and waits for it. scratch: device memory of at least CUs * (2048 + 16) bytes. */
+bool clef_hip_mfma_ceiling(int random, int iters, void *scratch, size_t scratch_bytes,
+                           double *tflops, double *ghz, char *err, size_t errlen);
 bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,
                             int32_t *sched, int max_sched, char *err, size_t errlen);
 
