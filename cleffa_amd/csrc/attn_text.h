@@ -5,9 +5,9 @@
 // sum of the rounded P, O / l * sigmoid(G)), metal/clef.metal:245-300 (prologue),
 // metal/clef.metal:709-849 (prefix: queries offset into the record's keys).
 //
-// Workgroup: 8 wavefronts (2 per SIMD), one block of 128 query rows of one q head; wave w owns
-// rows 16w .. 16w+15. Everything per wave lives in ~170 VGPRs (O^T 64, Q 32, S 16), so two
-// waves share a SIMD and one wave's softmax overlaps the other's matrix work.
+// Workgroup: 8 wavefronts (2 per SIMD), one block of 128 query rows of one q head per work item;
+// wave w owns rows 16w .. 16w+15. The state per wave (O^T 64, Q 32, S 16 VGPRs, operand rings,
+// addresses) fits 244 VGPRs, so two waves share a SIMD.
 //   S^T = K . Q^T      v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K from LDS,
 //                      B = the wave's Q (registers). A lane owns one query column. Q and K are
 //                      f16: their 11-bit significands keep the scores of sharp rows within the
@@ -266,8 +266,8 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
 
     // ---- first item's loads; q_norm (one element per thread) staged in LDS once
     Item cur = decode(item);
-    // Buffers of an item: its Q rows arrive in pair `qb`, its first key tile in the other pair
-    // (`par`), and the tiles alternate from there. The Q rows are issued first, then the rotary
+    // Buffers of an item: its first key tile arrives in buffer pair `par` (K and V^T buffers of
+    // that parity), its Q rows in the other pair, and the tiles alternate from there. The Q rows are issued first, then the rotary
     // cos/sin, then the first tile (8 loads per wave), so the prologue waits for the Q rows alone
     // and rotates them while the tile lands.
     int par = 0;
