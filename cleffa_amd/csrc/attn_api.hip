@@ -360,7 +360,7 @@ bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err,
         q.qkv = a->qkv; q.bias = a->bias; q.pos2 = a->pos2; q.inv_freq = a->inv_freq; q.kv_tok = a->kv_tok;
         q.q_plane = a->q_plane; q.k_plane = a->k_plane; q.vt_plane = a->vt_plane;
         q.P = a->P; q.heads = a->heads; q.kvT = a->kvT; q.kv_rows = a->kv_rows;
-        hipLaunchKernelGGL(vis_prep_kernel, dim3((a->kv_rows + 15) / 16, a->heads), dim3(256), 0, (hipStream_t)stream, q);
+        hipLaunchKernelGGL(vis_prep_kernel, dim3(((a->kv_rows + 15) / 16 * a->heads + 31) / 32 * 32), dim3(256), 0, (hipStream_t)stream, q);
         if (!launch_ok("vis_prep", err, errlen)) return false;
     }
     if (a->n_blk == 0) return true;

@@ -275,7 +275,14 @@ __global__ __launch_bounds__(256) void vis_prep_kernel(VisPrepParams p) {
     __shared__ int trow[ROWS];
     __shared__ float ang_pos[ROWS][2];
     const int tid = threadIdx.x, rr = tid >> 4, k = tid & 15;
-    const int r0 = blockIdx.x * ROWS, h = blockIdx.y;
+    // Work unit u = h * n_tiles + tile. Workgroup L runs on XCD L % 8 (round-robin dispatch);
+    // the four consecutive tiles whose 32-byte V^T runs share a 128-byte line go to four
+    // consecutive workgroups of one XCD, so the partial lines merge in that XCD's L2.
+    const int n_tiles = (p.kv_rows + ROWS - 1) / ROWS;
+    const int L = blockIdx.x, j = L >> 3;
+    const int u = 4 * (((j >> 2) << 3) + (L & 7)) + (j & 3);
+    if (u >= n_tiles * p.heads) return;
+    const int h = u / n_tiles, r0 = (u - h * n_tiles) * ROWS;
     const int E = p.heads * HD;
     // loads that do not depend on the row's patch go first: the lane's bias chunks and the
     // rotary frequencies of the pairs it turns
