@@ -152,7 +152,7 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
         // loads, so the search ends; on C1 it takes the makespan from 37 to 35 tiles.
         std::vector<int> wgs;
         for (int b = x; b < n_wg; b += groups) wgs.push_back(b);
-        for (int step = 0; step < 100000; step++) {
+        for (int step = 0; step < 100000; step++) {   // a cap on host time for adversarial plans
             int mx = wgs[0];
             for (int b : wgs)
                 if (load[b] > load[mx]) mx = b;
