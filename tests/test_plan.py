@@ -140,3 +140,18 @@ def test_schedule_errors():
     plan = AttnPlan(np.array([0, 100], np.int32), causal=True, device="cpu")
     ok, _, err = _sched(plan, 6, 4, 8)       # nh not a multiple of nkv
     assert not ok and "bad schedule" in err
+
+
+def test_schedule_local_search_reaches_c1_bound():
+    """C1 (24/4 heads, 256 workgroups): the greedy placement alone leaves a workgroup at 37 tiles
+    of modelled cost; the local search brings every workgroup to at most 35, the ceiling of the
+    per-workgroup mean (34.3), which no schedule can beat."""
+    lengths = [1160, 890, 730, 425, 472, 136, 179, 104]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    plan = AttnPlan(cu, causal=True, device="cpu")
+    ok, s, err = _sched(plan, 24, 4, 256)
+    assert ok, err
+    off, items = s[:257], s[257:]
+    cost = lambda it: (int(plan.blocks_host[it // 24][4]) + 63) // 64 + 3
+    loads = [sum(cost(it) for it in items[off[b]:off[b + 1]]) for b in range(256)]
+    assert sum(loads) == 8784 and max(loads) <= 35
