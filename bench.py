@@ -286,7 +286,7 @@ def mfma_ceiling(random, iters=4000):
     random or constant-pattern bf16 operands, and the shader clock it held."""
     import ctypes
     from cleffa_amd import _lib
-    lib = _lib.load()
+    lib = _lib.load_bench()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     scratch = torch.empty(cus * (2048 + 16), dtype=torch.uint8, device="cuda")
     tf, ghz = ctypes.c_double(0.0), ctypes.c_double(0.0)

@@ -11,6 +11,7 @@ from pathlib import Path
 LIB_PATH = Path(os.environ.get("CLEF_HIP_ATTN_LIB") or Path(__file__).resolve().parent / "libclef_hip_attn.so")
 
 OUT_BF16, OUT_F16, OUT_F32 = 0, 1, 2
+QKV_BF16 = 0
 BLOCK_Q = 128
 KV_ALIGN = 64
 BLOCK_INTS = 8
@@ -19,7 +20,7 @@ BLOCK_INTS = 8
 EXPORTS = (
     "clef_hip_attn_version", "clef_hip_attn_wave_size", "clef_hip_attn_init",
     "clef_hip_attn_plan_max_blocks", "clef_hip_attn_plan", "clef_hip_attn_sched_size",
-    "clef_hip_attn_schedule", "clef_hip_mfma_ceiling",
+    "clef_hip_attn_schedule",
     "clef_hip_rope_inv_freq", "clef_hip_vis_positions", "clef_hip_attn_prep_kv",
     "clef_hip_attn_core", "clef_hip_attn_prefill", "clef_hip_vis_attention",
     "clef_hip_record_positions", "clef_hip_pack_batch",
@@ -42,6 +43,7 @@ class AttnArgs(ctypes.Structure):
         ("kv_rows", c_int), ("causal", c_int), ("gate", c_int),
         ("out", c_void_p), ("out_type", c_int), ("f16_lim", c_float), ("ovf", c_void_p),
         ("trace", c_void_p), ("sched", c_void_p), ("n_wg", c_int),
+        ("seq_start", c_void_p), ("qkv_type", c_int),
     ]
 
 
@@ -120,9 +122,6 @@ def load():
                                        POINTER(c_int32), c_int,
                                        POINTER(c_int), POINTER(c_int), c_char_p, c_size_t]
     lib.clef_hip_attn_plan.restype = c_bool
-    lib.clef_hip_mfma_ceiling.argtypes = [c_int, c_int, c_void_p, c_size_t, POINTER(ctypes.c_double),
-                                          POINTER(ctypes.c_double), c_char_p, c_size_t]
-    lib.clef_hip_mfma_ceiling.restype = c_bool
     lib.clef_hip_attn_sched_size.argtypes = [c_int, c_int, c_int]
     lib.clef_hip_attn_sched_size.restype = c_int
     lib.clef_hip_attn_schedule.argtypes = [POINTER(c_int32), c_int, c_int, c_int, c_int, POINTER(c_int32), c_int,
@@ -140,6 +139,18 @@ def load():
     lib.clef_hip_vis_attention.argtypes = [POINTER(VisArgs), c_void_p, c_char_p, c_size_t]
     lib.clef_hip_vis_attention.restype = c_bool
     _lib = lib
+    return lib
+
+
+def load_bench():
+    """The measurement utility library (clef_hip_mfma_ceiling), built beside the product."""
+    path = LIB_PATH.parent / "libclef_hip_bench.so"
+    if not path.exists():
+        raise RuntimeError(f"{path} is not built: run `python -m cleffa_amd.build`")
+    lib = ctypes.CDLL(str(path))
+    lib.clef_hip_mfma_ceiling.argtypes = [c_int, c_int, c_void_p, c_size_t, POINTER(ctypes.c_double),
+                                          POINTER(ctypes.c_double), c_char_p, c_size_t]
+    lib.clef_hip_mfma_ceiling.restype = c_bool
     return lib
 
 

@@ -141,6 +141,10 @@ class AttnPlan:
         self.kv_tok = torch.from_numpy(np.ascontiguousarray(kv_tok[: max(self.kv_rows, 1)])).to(self.device)
         # kv rows the planes must hold, rounded to the 16-byte V^T chunk
         self.kvT = max(8, (self.kv_rows + 7) // 8 * 8)
+        # each pass row's record start (the reference's seq_start): where the K/V prologue flags
+        # a key that leaves f16's range
+        seq_start = np.repeat(cu_q[:-1], np.diff(cu_q)).astype(np.int32)
+        self.seq_start = torch.from_numpy(np.ascontiguousarray(seq_start if self.T else np.zeros(1, np.int32))).to(self.device)
 
     def schedule(self, nh, nkv, n_wg):
         """Per-workgroup item lists of the attention core over n_wg workgroups (device int32,
@@ -251,6 +255,7 @@ class TextAttention:
         a.causal, a.gate = int(plan.causal), int(gate)
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
         a.trace = _ptr(trace)
+        a.seq_start, a.qkv_type = _ptr(plan.seq_start), _lib.QKV_BF16
         if schedule and plan.n_blk:
             n_wg = _device_cus(dev)
             a.sched, a.n_wg = _ptr(plan.schedule(self.nh, self.nkv, n_wg)), n_wg

@@ -19,7 +19,8 @@ using namespace clef_hip;
 
 namespace {
 
-constexpr int kVersion = 1;
+constexpr int kVersion = 2;
+constexpr int32_t kSchedMagic = 0x53434844;   // header word of a schedule ('SCHD')
 constexpr int kVisHD = 72;
 
 bool fail(char *err, size_t errlen, const char *fmt, ...) {
@@ -44,6 +45,9 @@ bool launch_ok(const char *what, char *err, size_t errlen) {
     return true;
 }
 
+// The f16 overflow limit as the reference clamps it (clef_metal.m:237-238): (0, 65504], else 65504.
+float f16_limit(float lim) { return (lim > 0.f && lim <= 65504.f) ? lim : 65504.f; }
+
 bool rot_ok(int n_rot, int hd) {
     // the fused Q prologue is compiled for these rotary widths (Clef pins 64, clef.c:116-120)
     return (n_rot == 0 || n_rot == 64) && n_rot <= hd;
@@ -52,6 +56,8 @@ bool rot_ok(int n_rot, int hd) {
 bool check_text(const clef_hip_attn_args *a, bool need_core, char *err, size_t errlen) {
     if (!a) return fail(err, errlen, "null attention arguments");
     if (a->hd != 256) return fail(err, errlen, "text attention supports hd 256 only (got %d)", a->hd);
+    if (a->qkv_type != CLEF_HIP_QKV_BF16)
+        return fail(err, errlen, "qkv_type %d not supported: the qkv rows must be bf16 (write them so from the QKV GEMM)", a->qkv_type);
     if (a->nh <= 0 || a->nkv <= 0 || a->nh % a->nkv) return fail(err, errlen, "bad head counts nh=%d nkv=%d", a->nh, a->nkv);
     if (!rot_ok(a->n_rot, a->hd)) return fail(err, errlen, "unsupported n_rot %d", a->n_rot);
     if (a->T < 0 || a->n_blk < 0 || a->kv_rows < 0) return fail(err, errlen, "negative sizes");
@@ -114,14 +120,14 @@ bool clef_hip_attn_init(char *err, size_t errlen) {
 
 int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg) {
     if (n_blk < 0 || nh <= 0 || n_wg <= 0) return 0;
-    return n_wg + 1 + n_blk * nh;
+    return 4 + n_wg + 1 + n_blk * nh;
 }
 
 bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,
                             int32_t *sched, int max_sched, char *err, size_t errlen) {
     if ((n_blk && !blocks) || !sched || n_blk < 0 || nh <= 0 || nkv <= 0 || nh % nkv || n_wg <= 0)
         return fail(err, errlen, "bad schedule arguments");
-    const long need = (long)n_wg + 1 + (long)n_blk * nh;
+    const long need = 4L + n_wg + 1 + (long)n_blk * nh;
     if (need > max_sched) return fail(err, errlen, "schedule needs %ld entries, room for %d", need, max_sched);
     // cost of an item in 64-key tiles: its tiles plus the prologue / epilogue (Q rows, gate,
     // output stores), measured at about three tiles' time per item
@@ -184,12 +190,17 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
     }
     for (auto &l : lists)   // each workgroup takes its items longest first
         std::stable_sort(l.begin(), l.end(), [&](int u, int v) { return cost_of(u) > cost_of(v); });
+    sched[0] = kSchedMagic;
+    sched[1] = n_blk;
+    sched[2] = nh;
+    sched[3] = n_wg;
+    int32_t *const offs = sched + 4;
     int off = 0;
     for (int b = 0; b < n_wg; b++) {
-        sched[b] = off;
-        for (int it : lists[b]) sched[n_wg + 1 + off++] = it;
+        offs[b] = off;
+        for (int it : lists[b]) offs[n_wg + 1 + off++] = it;
     }
-    sched[n_wg] = off;
+    offs[n_wg] = off;
     return true;
 }
 
@@ -298,6 +309,7 @@ bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err,
     p.kv_tok = a->kv_tok; p.k_plane = a->k_plane; p.vt_plane = a->vt_plane;
     p.kv_rows = a->kv_rows; p.row = a->row; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
     p.eps = a->eps; p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
+    p.seq_start = a->seq_start; p.ovf = a->ovf; p.f16_lim = f16_limit(a->f16_lim);
     dim3 grid((a->kv_rows + kPrepRows - 1) / kPrepRows, a->nkv);
     hipLaunchKernelGGL(text_prep_kv_kernel, grid, dim3(16 * kPrepRows), 0, (hipStream_t)stream, p);
     return launch_ok("text_prep_kv", err, errlen);
@@ -313,7 +325,8 @@ bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, si
     p.k_plane = a->k_plane; p.vt_plane = a->vt_plane; p.blocks = a->blocks;
     p.out = a->out; p.ovf = a->ovf;
     p.row = a->row; p.T = a->T; p.kvT = a->kvT; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot;
-    p.eps = a->eps; p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = a->f16_lim;
+    p.eps = a->eps; p.scale_log2 = a->scale * 1.4426950408889634f;
+    p.f16_lim = f16_limit(a->f16_lim);
     p.causal = a->causal ? 1 : 0; p.gate = a->gate ? 1 : 0; p.out_type = a->out_type;
     p.out_ld = a->nh * a->hd;
     p.trace = a->trace;
@@ -369,7 +382,7 @@ bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err,
     p.q_plane = a->q_plane; p.k_plane = a->k_plane; p.vt_plane = a->vt_plane; p.blocks = a->blocks;
     p.out = a->out; p.ovf = a->ovf;
     p.T = a->P; p.kvT = a->kvT; p.nh = a->heads; p.nkv = a->heads;
-    p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = a->f16_lim;
+    p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = f16_limit(a->f16_lim);
     p.causal = 0; p.gate = 0; p.out_type = a->out_type; p.out_ld = a->heads * kVisHD;
     hipLaunchKernelGGL(attn_vis_kernel, dim3((unsigned)(a->n_blk * a->heads)), dim3(64 * vis::WAVES), 0, (hipStream_t)stream, p);
     return launch_ok("attn_vis", err, errlen);

@@ -148,6 +148,21 @@ __global__ __launch_bounds__(16 * kPrepRows) void text_prep_kv_kernel(PrepParams
         kw[h] = t >= 0 ? *(const u32x4 *)(src + 8 * h) : u32x4{0, 0, 0, 0};
         vw[h] = t >= 0 ? *(const u32x4 *)(src + (size_t)p.nkv * HD + 8 * h) : u32x4{0, 0, 0, 0};
     }
+    // A non-finite V element (bf16 exponent all ones) saturates to +-65536 (bf16's rounding of
+    // 65504) and flags the record, as split16 does for the reference's f16 V plane
+    // (metal/clef.metal:857-867): nothing past a record's own keys can then read inf or NaN.
+    bool bad = false;
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            unsigned w = vw[h][j];
+            const bool lo_bad = (w & 0x7f80u) == 0x7f80u, hi_bad = (w & 0x7f800000u) == 0x7f800000u;
+            if (lo_bad) w = (w & 0xffff8000u) | 0x4780u;
+            if (hi_bad) w = (w & 0x8000ffffu) | 0x47800000u;
+            bad |= lo_bad | hi_bad;
+            vw[h][j] = w;
+        }
     float wn[16];
     if (p.k_norm) {
 #pragma unroll
@@ -212,6 +227,19 @@ __global__ __launch_bounds__(16 * kPrepRows) void text_prep_kv_kernel(PrepParams
             }
         }
     }
+    // The f16 K plane follows split16: |k| > f16_lim or NaN saturates to +-65504 and flags the
+    // record (at its first pass row, seq_start).
+    {
+        const unsigned lim = __float_as_uint(p.f16_lim);
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const bool over = (__float_as_uint(x[e]) & 0x7fffffffu) > lim;
+            x[e] = over ? copysignf(65504.f, x[e]) : x[e];
+            bad |= over;
+        }
+    }
+    if (bad && t >= 0 && p.ovf && p.seq_start)
+        __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t >= 0) {
         uint16_t *dst = p.k_plane + ((size_t)kh * p.kvT + r0 + rr) * HD + 16 * k;
 #pragma unroll

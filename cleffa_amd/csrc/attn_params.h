@@ -24,7 +24,7 @@ struct AttnParams {
     int n_blk;                // blocks in the plan (work items = n_blk * nh)
     int xcd_heads;            // nh / 8 when heads split evenly over the 8 XCDs, else 0
     uint64_t *trace;          // NULL, or [n_blk * nh][8] per work item: start, end, HW_ID, XCC_ID, prologue end, loop end, workgroup, ordinal
-    const int32_t *sched;     // NULL, or per-workgroup item lists: [gridDim.x + 1] offsets, then items
+    const int32_t *sched;     // NULL, or a schedule: header {magic, n_blk, nh, n_wg}, [n_wg + 1] offsets, items
 };
 
 struct PrepParams {
@@ -36,8 +36,10 @@ struct PrepParams {
     uint16_t *k_plane;
     uint16_t *vt_plane;
     float *rope_cs;
+    const int32_t *seq_start; // record start of each pass row (overflow flags), or NULL
+    int32_t *ovf;
     int kv_rows, row, nh, nkv, n_rot, kvT;
-    float eps;
+    float eps, f16_lim;
 };
 
 struct VisPrepParams {

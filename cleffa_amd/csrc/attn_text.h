@@ -98,7 +98,8 @@ __device__ __forceinline__ void static_for(F &&f) {
 }  // namespace text
 
 // Work items are (query block, q head) pairs. Workgroup b takes items get(0), get(1), ... With a
-// host schedule (p.sched, clef_hip_attn_schedule) they are the workgroup's own list. Otherwise
+// host schedule (p.sched, clef_hip_attn_schedule) they are the workgroup's own list; an item
+// index outside the plan ends the list, so no list can make the kernel touch memory outside it. Otherwise
 // they come from a static order: with xcd_heads, the items of XCD x (workgroup ids go round-robin
 // over the 8 XCDs, each with its own L2) are the heads x*xcd_heads .. +xcd_heads-1 of every block,
 // so an XCD streams the K/V of as few kv heads as possible; items keep the plan's longest-first
@@ -123,15 +124,21 @@ struct ItemList {
         per_x = xh ? p.n_blk * xh : 0;
         list = nullptr;
         s0 = s1 = 0;
+        // a schedule: header {magic, n_blk, nh, n_wg}, then offsets and items
         if (p.sched) {
-            s0 = sload(p.sched + blockIdx.x);
-            s1 = sload(p.sched + blockIdx.x + 1);
-            list = p.sched + gridDim.x + 1;
+            const int32_t *offs = p.sched + 4;
+            s0 = sload(offs + blockIdx.x);
+            s1 = sload(offs + blockIdx.x + 1);
+            list = offs + gridDim.x + 1;
         }
     }
     // the k-th item of this workgroup as block * nh + head, or -1
     __device__ __forceinline__ int get(int k) const {
-        if (list) return s0 + k < s1 ? sload(list + s0 + k) : -1;
+        if (list) {
+            if (s0 + k >= s1) return -1;
+            const int it = sload(list + s0 + k);
+            return (it >= 0 && it < n_items) ? it : -1;   // never an item outside the plan
+        }
         if (xh && gx && ((int)gridDim.x & 7) == 0) {
             const int x = blockIdx.x & 7, wl = blockIdx.x >> 3;
             const int j = k * gx + ((k & 1) ? gx - 1 - wl : wl);
@@ -385,15 +392,39 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                     }
                 }
             }
+            // Scaled by scale * log2 e before the one rounding to f16: the products give scores in
+            // the exp2 domain. The f16 operand follows split16 (metal/clef.metal:857-867): an
+            // element with |q| > f16_lim or NaN flags the record, and the operand saturates.
+            // Normalised rows are bounded by 16 max|w|; only a row that is not finite (its sum of
+            // squares) can flag. Plain rows are checked element by element (the largest
+            // magnitude's bits, which order NaN above every number) and clamped.
+            const float sc = p.scale_log2;
+            bool q_bad;
+            if (p.q_norm) {
+                q_bad = !(ss <= 3.0e38f);
 #pragma unroll
-            for (int c = 0; c < NC; c++) {
-                // scaled by scale * log2 e before the one rounding to f16: the products give
-                // scores in the exp2 domain
-                const float sc = p.scale_log2;
-                u32x4 w = {pack_f16(x[c][0] * sc, x[c][1] * sc), pack_f16(x[c][2] * sc, x[c][3] * sc),
-                           pack_f16(x[c][4] * sc, x[c][5] * sc), pack_f16(x[c][6] * sc, x[c][7] * sc)};
-                qf[c] = __builtin_bit_cast(f16x8, w);
+                for (int c = 0; c < NC; c++) {
+                    u32x4 w = {pack_f16(x[c][0] * sc, x[c][1] * sc), pack_f16(x[c][2] * sc, x[c][3] * sc),
+                               pack_f16(x[c][4] * sc, x[c][5] * sc), pack_f16(x[c][6] * sc, x[c][7] * sc)};
+                    qf[c] = __builtin_bit_cast(f16x8, w);
+                }
+            } else {
+                unsigned amax = 0;
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    float y[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        amax = max(amax, __float_as_uint(x[c][j]) & 0x7fffffffu);
+                        y[j] = __builtin_amdgcn_fmed3f(x[c][j] * sc, -65504.f, 65504.f);
+                    }
+                    u32x4 w = {pack_f16(y[0], y[1]), pack_f16(y[2], y[3]), pack_f16(y[4], y[5]), pack_f16(y[6], y[7])};
+                    qf[c] = __builtin_bit_cast(f16x8, w);
+                }
+                q_bad = amax > __float_as_uint(p.f16_lim);
             }
+            if (q_bad && q_valid && p.ovf)
+                __hip_atomic_store(p.ovf + cur.flag_row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
 
         f32x4 o[16];

@@ -3,7 +3,14 @@
 // waves per CU, 4 accumulators per wave, LDS reads 6 ahead. With random bf16 operands the part
 // draws more power than with a constant bit pattern and holds a lower shader clock, so the
 // random-operand rate is what the matrix cores sustain on attention data. A measurement utility
-// with no reference counterpart.
+// with no reference counterpart, built into its own library (libclef_hip_bench.so, used by
+// bench.py), apart from the engine-facing one.
+//
+// bool clef_hip_mfma_ceiling(int random, int iters, void *scratch, size_t scratch_bytes,
+//                            double *tflops, double *ghz, char *err, size_t errlen);
+// Runs on the default stream and waits for it; scratch: device memory of at least
+// CUs * (2048 + 16) bytes; writes the sustained TF/s and the shader clock it held (cycle counter
+// against the 100 MHz wall clock). Returns false with "hip: ..." in err on failure.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -11,7 +18,6 @@
 
 #include <utility>
 
-#include "clef_hip_attn.h"
 
 namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;

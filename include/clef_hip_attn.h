@@ -110,7 +110,12 @@ typedef struct {
     int gate;                 /* 1: multiply by sigmoid(gate) (Qwen3.5 gated attention) */
     void *out;                /* [T][nh*hd] */
     int out_type;             /* CLEF_HIP_OUT_* */
-    float f16_lim;            /* overflow limit for CLEF_HIP_OUT_F16 (65504) */
+    float f16_lim;            /* f16 overflow limit (65504): the K plane and Q operand are f16, so
+                                 a key or query element with |x| > f16_lim or NaN is saturated to
+                                 +-65504 and flags its record, as split16 does
+                                 (metal/clef.metal:857-867); so does an f16 output (act16) with
+                                 CLEF_HIP_OUT_F16. Non-finite V elements (V is bf16 here) are
+                                 saturated to +-65504 and flag too */
     int32_t *ovf;             /* [T] int32 flags, set at the record's first pass row; may be NULL */
     uint64_t *trace;          /* NULL, or [n_blk * nh][8] u64 per work item (query block, q head):
                                  start, end (100 MHz device wall clock), HW_ID and XCC_ID
@@ -119,9 +124,22 @@ typedef struct {
                                  (clef_metal.m:52-68) at work-item grain */
     const int32_t *sched;     /* NULL, or device copy of clef_hip_attn_schedule's output for this
                                  plan, nh and n_wg: the core then runs n_wg workgroups, each
-                                 over its own item list */
+                                 over its own item list. A list built for another plan, nh or
+                                 n_wg gives undefined output (its header names the (n_blk, nh,
+                                 n_wg) it was built for); the kernel never runs an item index
+                                 outside this plan, so it cannot reach memory outside it */
     int n_wg;
+    const int32_t *seq_start; /* [T] device int32: each pass row's record start (the reference's
+                                 seq_start, clef_engine.h:179), where prep_kv flags a key that
+                                 leaves f16's range (see f16_lim); NULL: such keys are still
+                                 saturated, but not flagged */
+    int qkv_type;             /* CLEF_HIP_QKV_BF16 (0), the only row type taken: the reference's
+                                 f32 rows (clef.metal:252) come from a QKV GEMM that writes bf16
+                                 here (clef_hip_gemm y_type CLEF_HIP_GEMM_Y_BF16); any other value
+                                 is rejected with an error */
 } clef_hip_attn_args;
+
+#define CLEF_HIP_QKV_BF16 0
 
 /* Static split of a text pass's work items (query block, q head) over n_wg workgroups of the
  * attention core, for clef_hip_attn_args.sched. No reference counterpart: the Metal backend
@@ -129,18 +147,11 @@ typedef struct {
  * the split made on the host. Items are dealt longest first to the least loaded workgroup
  * (cost: the block's 64-key tiles plus a fixed per-item cost), within the workgroups of the XCD
  * that owns the item's q head when the heads divide evenly over the 8 XCDs (workgroup b runs on
- * XCD b % 8). blocks: the plan's host block list. Output: sched[0..n_wg] item offsets per
- * workgroup, then the items as block * nh + head, each workgroup's longest first;
- * clef_hip_attn_sched_size gives the entry count. */
+ * XCD b % 8). blocks: the plan's host block list. Output: a header {0x53434844, n_blk, nh,
+ * n_wg}, then n_wg + 1 item offsets per workgroup, then the items as block * nh + head, each
+ * workgroup's longest first; clef_hip_attn_sched_size gives the entry count. */
 int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg);
 
-/* Measurement utility, no reference counterpart: the MFMA rate the attention kernels' operand
- * stream sustains on this device (v_mfma_f32_16x16x32_bf16, one ds_read_b128 A operand per
- * product, 8 waves per CU), with random (random != 0) or constant-pattern bf16 operands, and the
- * shader clock it held (cycle counter against the 100 MHz wall clock). Runs on the default
- * stream and waits for it. scratch: device memory of at least CUs * (2048 + 16) bytes. */
-bool clef_hip_mfma_ceiling(int random, int iters, void *scratch, size_t scratch_bytes,
-                           double *tflops, double *ghz, char *err, size_t errlen);
 bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,
                             int32_t *sched, int max_sched, char *err, size_t errlen);
 

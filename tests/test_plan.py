@@ -114,6 +114,8 @@ def test_schedule_covers_items_balanced(lengths, nh, nkv, n_wg):
     plan = AttnPlan(cu, causal=True, device="cpu")
     ok, s, err = _sched(plan, nh, nkv, n_wg)
     assert ok, err
+    assert s[:4].tolist() == [0x53434844, plan.n_blk, nh, n_wg]   # the header the kernel checks
+    s = s[4:]
     off, items = s[: n_wg + 1], s[n_wg + 1:]
     assert off[0] == 0 and (np.diff(off) >= 0).all() and off[-1] == plan.n_blk * nh
     assert sorted(items.tolist()) == list(range(plan.n_blk * nh))
@@ -151,7 +153,7 @@ def test_schedule_local_search_reaches_c1_bound():
     plan = AttnPlan(cu, causal=True, device="cpu")
     ok, s, err = _sched(plan, 24, 4, 256)
     assert ok, err
-    off, items = s[:257], s[257:]
+    off, items = s[4:261], s[261:]
     cost = lambda it: (int(plan.blocks_host[it // 24][4]) + 63) // 64 + 3
     loads = [sum(cost(it) for it in items[off[b]:off[b + 1]]) for b in range(256)]
     assert sum(loads) == 8784 and max(loads) <= 35
