@@ -12,6 +12,7 @@ LIB_PATH = Path(os.environ.get("CLEF_HIP_ATTN_LIB") or Path(__file__).resolve().
 
 OUT_BF16, OUT_F16, OUT_F32 = 0, 1, 2
 QKV_BF16 = 0
+VIS_SCRATCH_BYTES = 64 << 20
 BLOCK_Q = 128
 KV_ALIGN = 64
 BLOCK_INTS = 8
@@ -22,7 +23,7 @@ EXPORTS = (
     "clef_hip_attn_plan_max_blocks", "clef_hip_attn_plan", "clef_hip_attn_sched_size",
     "clef_hip_attn_schedule",
     "clef_hip_rope_inv_freq", "clef_hip_vis_positions", "clef_hip_attn_prep_kv",
-    "clef_hip_attn_core", "clef_hip_attn_prefill", "clef_hip_vis_attention",
+    "clef_hip_attn_core", "clef_hip_attn_prefill", "clef_hip_vis_attention", "clef_hip_vis_attention_noalloc",
     "clef_hip_record_positions", "clef_hip_pack_batch",
     "clef_hip_gemm",
     "clef_hip_omni_rope_table", "clef_hip_omni_prep", "clef_hip_omni_plan_max_blocks",
@@ -136,8 +137,10 @@ def load():
         fn = getattr(lib, name)
         fn.argtypes = [POINTER(AttnArgs), c_void_p, c_char_p, c_size_t]
         fn.restype = c_bool
-    lib.clef_hip_vis_attention.argtypes = [POINTER(VisArgs), c_void_p, c_char_p, c_size_t]
-    lib.clef_hip_vis_attention.restype = c_bool
+    for name in ("clef_hip_vis_attention", "clef_hip_vis_attention_noalloc"):
+        fn = getattr(lib, name)
+        fn.argtypes = [POINTER(VisArgs), c_void_p, c_char_p, c_size_t]
+        fn.restype = c_bool
     _lib = lib
     return lib
 

@@ -301,7 +301,9 @@ class VisionAttention:
         self.inv_freq = torch.from_numpy(rope_inv_freq(theta, hd // 2).copy()).to(self.device)
 
     def forward(self, qkv, bias, pos2, plan, out=None, out_dtype="bf16", ovf=None,
-                f16_lim=65504.0, stream=None, scratch=None):
+                f16_lim=65504.0, stream=None, scratch=None, noalloc=False):
+        """noalloc: run clef_hip_vis_attention_noalloc, whose planes are the library's own
+        device scratch (no plane tensors are made; `out` is still allocated here if None)."""
         lib = _lib.load()
         if plan.causal or plan.cu_k is not None:
             raise ValueError("vision attention takes a bidirectional fresh plan")
@@ -317,12 +319,15 @@ class VisionAttention:
         if ovf is not None:
             _check(ovf, "ovf", (P,), torch.int32, dev)
         kvT = plan.kvT
-        if scratch is None:
-            scratch = self.scratch(P, kvT)
-        q_plane, k_plane, vt_plane = scratch
-        _check(q_plane, "q_plane", (self.heads, P, self.hd), torch.bfloat16, dev)
-        _check(k_plane, "k_plane", (self.heads, kvT, self.hd), torch.bfloat16, dev)
-        _check(vt_plane, "vt_plane", (self.heads, self.hd, kvT), torch.bfloat16, dev)
+        if noalloc:
+            q_plane = k_plane = vt_plane = None
+        else:
+            if scratch is None:
+                scratch = self.scratch(P, kvT)
+            q_plane, k_plane, vt_plane = scratch
+            _check(q_plane, "q_plane", (self.heads, P, self.hd), torch.bfloat16, dev)
+            _check(k_plane, "k_plane", (self.heads, kvT, self.hd), torch.bfloat16, dev)
+            _check(vt_plane, "vt_plane", (self.heads, self.hd, kvT), torch.bfloat16, dev)
         a = VisArgs()
         a.P, a.heads, a.hd, a.scale = P, self.heads, self.hd, self.scale
         a.qkv, a.bias, a.pos2, a.inv_freq = _ptr(qkv), _ptr(bias), _ptr(pos2), _ptr(self.inv_freq)
@@ -330,7 +335,8 @@ class VisionAttention:
         a.blocks, a.n_blk, a.kv_tok, a.kv_rows = _ptr(plan.blocks), plan.n_blk, _ptr(plan.kv_tok), plan.kv_rows
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
         err = _err()
-        _lib.check(lib.clef_hip_vis_attention(ctypes.byref(a), _stream_handle(stream), err, len(err)), err)
+        fn = lib.clef_hip_vis_attention_noalloc if noalloc else lib.clef_hip_vis_attention
+        _lib.check(fn(ctypes.byref(a), _stream_handle(stream), err, len(err)), err)
         return out
 
     def scratch(self, P, kvT):

@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "attn_kernels.h"
@@ -16,6 +17,9 @@
 #include "clef_hip_attn.h"
 
 using namespace clef_hip;
+
+// Device scratch of clef_hip_vis_attention_noalloc: the three vision planes, one copy per GPU.
+static __device__ __align__(256) unsigned char scratch[CLEF_HIP_VIS_SCRATCH_BYTES];
 
 namespace {
 
@@ -97,6 +101,68 @@ long device_cus() {
     return n;
 }
 
+
+// ---- Library-owned vision scratch (clef_hip_vis_attention_noalloc). The array's name is a
+// host-side stand-in: its device address on each GPU comes from hipGetSymbolAddress, taken once
+// per device with that device current, and only that address is handed to kernels.
+constexpr size_t kVisScratchBytes = CLEF_HIP_VIS_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char *g_scratch_ptr[kMaxDevices];
+
+// Bytes of one [heads][rows][72] bf16 plane, rounded up to 256 so the next plane stays aligned.
+size_t vis_plane_bytes(int heads, int rows) {
+    return ((size_t)heads * (size_t)rows * kVisHD * sizeof(uint16_t) + 255) & ~(size_t)255;
+}
+
+bool scratch_base(char **out, char *err, size_t errlen) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(err, errlen, "no device: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(err, errlen, "device %d beyond the scratch table", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) return fail(err, errlen, "scratch address on device %d: %s", dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = (char *)ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return true;
+}
+
+// The vision step on the given planes (the caller's, or the library's scratch).
+bool vis_run(const clef_hip_vis_args *a, uint16_t *q_plane, uint16_t *k_plane, uint16_t *vt_plane, void *stream,
+             char *err, size_t errlen) {
+    if (a->hd != kVisHD) return fail(err, errlen, "vision attention supports hd 72 only (got %d)", a->hd);
+    if (a->P < 0 || a->heads <= 0 || a->n_blk < 0 || a->kv_rows < 0) return fail(err, errlen, "bad vision sizes");
+    if (a->kvT % 8 || a->kvT < a->kv_rows) return fail(err, errlen, "kvT %d must be a multiple of 8 and >= kv_rows %d", a->kvT, a->kv_rows);
+    if (!a->qkv || !a->pos2 || !a->inv_freq || !q_plane || !k_plane || !vt_plane || !a->out)
+        return fail(err, errlen, "missing vision buffer");
+    if (!aligned16(q_plane) || !aligned16(k_plane) || !aligned16(vt_plane) || !aligned16(a->out))
+        return fail(err, errlen, "vision planes and output must be 16-byte aligned");
+    if (a->out_type < CLEF_HIP_OUT_BF16 || a->out_type > CLEF_HIP_OUT_F32) return fail(err, errlen, "bad out_type %d", a->out_type);
+    if ((a->n_blk && !a->blocks) || (a->kv_rows && !a->kv_tok)) return fail(err, errlen, "missing plan");
+    if (a->P && a->kv_rows) {
+        VisPrepParams q;
+        q.qkv = a->qkv; q.bias = a->bias; q.pos2 = a->pos2; q.inv_freq = a->inv_freq; q.kv_tok = a->kv_tok;
+        q.q_plane = q_plane; q.k_plane = k_plane; q.vt_plane = vt_plane;
+        q.P = a->P; q.heads = a->heads; q.kvT = a->kvT; q.kv_rows = a->kv_rows;
+        hipLaunchKernelGGL(vis_prep_kernel, dim3(((a->kv_rows + 15) / 16 * a->heads + 31) / 32 * 32), dim3(256), 0, (hipStream_t)stream, q);
+        if (!launch_ok("vis_prep", err, errlen)) return false;
+    }
+    if (a->n_blk == 0) return true;
+    AttnParams p;
+    memset(&p, 0, sizeof(p));
+    p.q_plane = q_plane; p.k_plane = k_plane; p.vt_plane = vt_plane; p.blocks = a->blocks;
+    p.out = a->out; p.ovf = a->ovf;
+    p.T = a->P; p.kvT = a->kvT; p.nh = a->heads; p.nkv = a->heads;
+    p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = f16_limit(a->f16_lim);
+    p.causal = 0; p.gate = 0; p.out_type = a->out_type; p.out_ld = a->heads * kVisHD;
+    hipLaunchKernelGGL(attn_vis_kernel, dim3((unsigned)(a->n_blk * a->heads)), dim3(64 * vis::WAVES), 0, (hipStream_t)stream, p);
+    return launch_ok("attn_vis", err, errlen);
+}
+
 }  // namespace
 
 extern "C" {
@@ -115,7 +181,8 @@ bool clef_hip_attn_init(char *err, size_t errlen) {
     if (prop.warpSize != 64) return fail(err, errlen, "attention kernels need 64-wide wavefronts (device reports %d)", prop.warpSize);
     const size_t need = sizeof(uint16_t) * text::LDS_ELEMS;
     if (prop.sharedMemPerBlock < need) return fail(err, errlen, "device LDS %zu < %zu bytes", (size_t)prop.sharedMemPerBlock, need);
-    return true;
+    char *scratch_ptr = nullptr;   // resolve this device's scratch address now, not on a first call
+    return scratch_base(&scratch_ptr, err, errlen);
 }
 
 int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg) {
@@ -359,33 +426,21 @@ bool clef_hip_attn_prefill(const clef_hip_attn_args *a, void *stream, char *err,
 
 bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen) {
     if (!a) return fail(err, errlen, "null vision arguments");
+    return vis_run(a, a->q_plane, a->k_plane, a->vt_plane, stream, err, errlen);
+}
+
+bool clef_hip_vis_attention_noalloc(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen) {
+    if (!a) return fail(err, errlen, "null vision arguments");
     if (a->hd != kVisHD) return fail(err, errlen, "vision attention supports hd 72 only (got %d)", a->hd);
-    if (a->P < 0 || a->heads <= 0 || a->n_blk < 0 || a->kv_rows < 0) return fail(err, errlen, "bad vision sizes");
-    if (a->kvT % 8 || a->kvT < a->kv_rows) return fail(err, errlen, "kvT %d must be a multiple of 8 and >= kv_rows %d", a->kvT, a->kv_rows);
-    if (!a->qkv || !a->pos2 || !a->inv_freq || !a->q_plane || !a->k_plane || !a->vt_plane || !a->out)
-        return fail(err, errlen, "missing vision buffer");
-    if (!aligned16(a->q_plane) || !aligned16(a->k_plane) || !aligned16(a->vt_plane) || !aligned16(a->out))
-        return fail(err, errlen, "vision planes and output must be 16-byte aligned");
-    if (a->out_type < CLEF_HIP_OUT_BF16 || a->out_type > CLEF_HIP_OUT_F32) return fail(err, errlen, "bad out_type %d", a->out_type);
-    if ((a->n_blk && !a->blocks) || (a->kv_rows && !a->kv_tok)) return fail(err, errlen, "missing plan");
-    if (a->P && a->kv_rows) {
-        VisPrepParams q;
-        q.qkv = a->qkv; q.bias = a->bias; q.pos2 = a->pos2; q.inv_freq = a->inv_freq; q.kv_tok = a->kv_tok;
-        q.q_plane = a->q_plane; q.k_plane = a->k_plane; q.vt_plane = a->vt_plane;
-        q.P = a->P; q.heads = a->heads; q.kvT = a->kvT; q.kv_rows = a->kv_rows;
-        hipLaunchKernelGGL(vis_prep_kernel, dim3(((a->kv_rows + 15) / 16 * a->heads + 31) / 32 * 32), dim3(256), 0, (hipStream_t)stream, q);
-        if (!launch_ok("vis_prep", err, errlen)) return false;
-    }
-    if (a->n_blk == 0) return true;
-    AttnParams p;
-    memset(&p, 0, sizeof(p));
-    p.q_plane = a->q_plane; p.k_plane = a->k_plane; p.vt_plane = a->vt_plane; p.blocks = a->blocks;
-    p.out = a->out; p.ovf = a->ovf;
-    p.T = a->P; p.kvT = a->kvT; p.nh = a->heads; p.nkv = a->heads;
-    p.scale_log2 = a->scale * 1.4426950408889634f; p.f16_lim = f16_limit(a->f16_lim);
-    p.causal = 0; p.gate = 0; p.out_type = a->out_type; p.out_ld = a->heads * kVisHD;
-    hipLaunchKernelGGL(attn_vis_kernel, dim3((unsigned)(a->n_blk * a->heads)), dim3(64 * vis::WAVES), 0, (hipStream_t)stream, p);
-    return launch_ok("attn_vis", err, errlen);
+    if (a->P < 0 || a->heads <= 0 || a->kvT < 0) return fail(err, errlen, "bad vision sizes");
+    const size_t qb = vis_plane_bytes(a->heads, a->P > 0 ? a->P : 1), kb = vis_plane_bytes(a->heads, a->kvT);
+    const size_t need = qb + 2 * kb;
+    if (need > kVisScratchBytes)
+        return fail(err, errlen, "vision planes need %zu bytes (heads %d, P %d, kvT %d): above the %zu-byte scratch",
+                    need, a->heads, a->P, a->kvT, kVisScratchBytes);
+    char *base = nullptr;
+    if (!scratch_base(&base, err, errlen)) return false;
+    return vis_run(a, (uint16_t *)base, (uint16_t *)(base + qb), (uint16_t *)(base + qb + kb), stream, err, errlen);
 }
 
 }  // extern "C"

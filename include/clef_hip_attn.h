@@ -189,6 +189,18 @@ typedef struct {
 
 bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen);
 
+/* clef_hip_vis_attention with the three planes in the library's own device scratch: it has no
+ * counterpart in the reference (whose vision planes are Metal buffers the backend owns), and is
+ * for callers that cannot allocate device memory (code under graph capture, serving loops,
+ * harnesses that forbid hipMalloc). q_plane, k_plane and vt_plane are ignored; the other fields
+ * mean what they mean above. The planes need heads * (max(P, 1) + 2 kvT) * 144 bytes (each plane
+ * rounded up to 256), at most CLEF_HIP_VIS_SCRATCH_BYTES; larger calls fail with an error. The
+ * scratch is one static array per GPU, held until the process ends and shared by every call on
+ * that GPU: calls that overlap on one GPU (other streams, other threads) race and must be
+ * serialised by the caller. Nothing in it needs clearing between calls. Allocates nothing. */
+#define CLEF_HIP_VIS_SCRATCH_BYTES ((size_t)64 << 20)
+bool clef_hip_vis_attention_noalloc(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen);
+
 /* ---- The GEMMs either side of the path (clef_metal.m:463-499 clef_metal_gemm; callers
  * clef_metal.m:1326 QKV projection, 1415 o_proj into the residual).
  * Y[T][N] (+)= X[T][K] . W[N][K]^T with X and W bf16 row-major, f32 accumulation. y_type
