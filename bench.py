@@ -52,6 +52,9 @@ def parse():
                     help="C0-C4: attention configurations; P: prefix-cache growth copy (HBM-bound); "
                          "O: Omni attention (hd 128, FP32, 16,344 tokens); G: the QKV and o_proj GEMMs around C1")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--fp32", action="store_true",
+                    help="C0-C3 in the FP32 mode (f32 qkv rows, FP32 planes and products: the reference's "
+                         "FP32 kernels); the roofline is then priced against the fp32 MFMA peak")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
     ap.add_argument("--profile-pass", action="store_true",
@@ -60,11 +63,15 @@ def parse():
     return ap.parse_args()
 
 
-def build_step(cfg, seed):
+def build_step(cfg, seed, fp32=False):
     """Returns (step_fn, core_fn, info) for one configuration, inputs resident on cuda:0."""
     from cleffa_amd import AttnPlan, TextAttention, VisionAttention, workloads
     dev = torch.device("cuda", 0)
     w = workloads.config(cfg, seed=seed, device=dev)
+    if fp32:
+        if cfg == "C4":
+            raise SystemExit("--fp32 applies to the text configurations C0-C3")
+        w["qkv"] = w["qkv"].float()
     if cfg == "C4":
         vis = VisionAttention(w["heads"], w["hd"], device=dev)
         plan = AttnPlan(w["cu_seqlens"], causal=False, device=dev)
@@ -78,13 +85,16 @@ def build_step(cfg, seed):
     att = TextAttention(w["nh"], w["nkv"], w["hd"], w["n_rot"], rope_theta=w["theta"], device=dev)
     if cfg == "C3":
         plan = AttnPlan(w["cu_seqlens"], w["cu_seqlens_k"], causal=True, device=dev)
-        kp = w["k_cache"].half().contiguous()   # f16 K plane
-        vt = w["v_cache"].transpose(1, 2).contiguous()
+        if fp32:
+            kp, vt = w["k_cache"].float().contiguous(), w["v_cache"].float().contiguous()
+        else:
+            kp = w["k_cache"].half().contiguous()   # f16 K plane
+            vt = w["v_cache"].transpose(1, 2).contiguous()
         kvT = kp.shape[1]
     else:
         plan = AttnPlan(w["cu_seqlens"], causal=True, device=dev)
         kvT = plan.kvT
-        kp, vt = att.planes(kvT)
+        kp, vt = att.planes(kvT, fp32=fp32)
     out = torch.empty((plan.T, w["nh"] * w["hd"]), dtype=torch.bfloat16, device=dev)
     kwargs = dict(out=out, gate=w["gate"], k_plane=kp, vt_plane=vt, kvT=kvT,
                   rope_cs=att.rope_table(plan.T) if w["n_rot"] else None)
@@ -93,9 +103,10 @@ def build_step(cfg, seed):
     core = lambda: att.forward(*args, stage="core", **kwargs)
     T, nh, nkv, hd = plan.T, w["nh"], w["nkv"], w["hd"]
     # algorithmic bytes: qkv rows read once, O written once, cached K/V read (C3)
-    nbytes = T * (2 * nh + 2 * nkv) * hd * 2 + T * nh * hd * 2
+    esz = 4 if fp32 else 2
+    nbytes = T * (2 * nh + 2 * nkv) * hd * esz + T * nh * hd * 2
     if cfg == "C3":
-        nbytes += 2 * nkv * (int(w["cu_seqlens_k"][-1]) - T) * hd * 2
+        nbytes += 2 * nkv * (int(w["cu_seqlens_k"][-1]) - T) * hd * esz
     names = {"C0": "C0 one causal 1,024-token record, 16/4 heads, hd 256, plain SDPA operands (no norm, "
                    "rotary or gate)",
              "C1": "C1 packed varlen causal micro-batch: 8 records, 4,096 tokens, 24/4 heads, hd 256, "
@@ -304,7 +315,7 @@ def bench_mfma_ceiling(a):
         "metric": "MFMA ceiling of the attention operand stream (v_mfma_f32_16x16x32_bf16, one "
                   "ds_read_b128 A operand per product, 8 waves per CU)",
         "value": round(r_tf, 1), "unit": "TFLOP/s", "n_gpus": 1, "higher_is_better": True,
-        "dtype": "bf16", "data": "synthetic: random bf16 operands (the value) and a constant bit pattern",
+        "dtype": "f32" if a.fp32 else "bf16", "data": "synthetic: random bf16 operands (the value) and a constant bit pattern",
         "config": {"workload": "MFMA ceiling, random and constant operands"},
         "random": {"tflops": round(r_tf, 1), "clock_ghz": round(r_ghz, 3), "frac": round(r_tf / PEAK_BF16_TFLOPS, 4)},
         "constant": {"tflops": round(c_tf, 1), "clock_ghz": round(c_ghz, 3), "frac": round(c_tf / PEAK_BF16_TFLOPS, 4)},
@@ -330,7 +341,7 @@ def main():
         return bench_gemms(a)
     if a.config == "M":
         return bench_mfma_ceiling(a)
-    step, core, info, w = build_step(a.config, a.seed)
+    step, core, info, w = build_step(a.config, a.seed, a.fp32)
     if a.profile_pass:
         src = torch.randn(CALIB_BYTES // 2, device="cuda").to(torch.bfloat16)
         dst = torch.empty_like(src)
@@ -347,7 +358,7 @@ def main():
     tflops = flops / (ms * 1e-3) / 1e12
     res = {
         "metric": "prefill attention TFLOP/s (4096-tok packed causal GQA micro-batch, hd 256)"
-        if a.config == "C1" else f"prefill attention TFLOP/s ({a.config})",
+        if a.config == "C1" and not a.fp32 else f"prefill attention TFLOP/s ({a.config}{', FP32 mode' if a.fp32 else ''})",
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "tokens_per_s": round(info["tokens"] / (ms * 1e-3), 1),
@@ -355,7 +366,7 @@ def main():
         "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms, 5), "host_ms_per_step": round(wall_ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs, random-init norm weights)",
+        "dtype": "f32" if a.fp32 else "bf16", "data": "synthetic (seeded N(0,1) inputs, random-init norm weights)",
         "config": {"workload": info["workload"], "seed": a.seed, "tokens": info["tokens"],
                    "pairs": info["pairs"], "gflop": round(flops / 1e9, 3),
                    **({"lengths": info["lengths"]} if "lengths" in info else {})},
@@ -363,19 +374,23 @@ def main():
     if core is not None:
         core_ms, _ = time_fn(core, a.steps, a.warmup, graph)
         achieved = flops / (core_ms * 1e-3) / 1e12
-        res["roofline"] = {"bound": "mfma", "kernel": "attn_text_kernel<64>",
-                           "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                           "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(a.config),
+        peak = PEAK_F32_MFMA if a.fp32 else PEAK_BF16_TFLOPS
+        kname = f"attn_text_f32_kernel<{info['nh'] // w['nkv']}>" if a.fp32 else "attn_text_kernel<64>"
+        res["roofline"] = {"bound": "mfma", "kernel": kname,
+                           "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                           "frac": round(achieved / peak, 4),
+                           "traffic": None if a.fp32 else measured_traffic(a.config),
                            "launch_ms": round(core_ms, 5),
                            "algorithmic_bytes": info["bytes"],
                            "hbm_frac_at_this_time": round(info["bytes"] / (core_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
         # the same MFMA operand stream with random operands, measured now on this device: the
         # rate the part's power and clock allow (the nominal peak assumes 2.4 GHz)
-        ceil_tf, ceil_ghz = mfma_ceiling(True)
-        res["roofline"].update({"mfma_stream_ceiling": round(ceil_tf, 1), "mfma_stream_clock_ghz": round(ceil_ghz, 3),
-                                "frac_of_stream_ceiling": round(achieved / ceil_tf, 4)})
+        if not a.fp32:
+            ceil_tf, ceil_ghz = mfma_ceiling(True)
+            res["roofline"].update({"mfma_stream_ceiling": round(ceil_tf, 1), "mfma_stream_clock_ghz": round(ceil_ghz, 3),
+                                    "frac_of_stream_ceiling": round(achieved / ceil_tf, 4)})
         res["prep_ms"] = round(ms - core_ms, 5)
-    if not a.no_cpu and a.config in ("C1", "C2") and a.config == "C1":
+    if not a.no_cpu and a.config == "C1" and not a.fp32:
         sec, threads = cpu_baseline(w, a.config)
         res["cpu_baseline"] = {"value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s",
                                "tokens_per_s": round(info["tokens"] / sec, 1), "ms": round(sec * 1e3, 2),

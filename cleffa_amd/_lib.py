@@ -11,7 +11,7 @@ from pathlib import Path
 LIB_PATH = Path(os.environ.get("CLEF_HIP_ATTN_LIB") or Path(__file__).resolve().parent / "libclef_hip_attn.so")
 
 OUT_BF16, OUT_F16, OUT_F32 = 0, 1, 2
-QKV_BF16 = 0
+QKV_BF16, QKV_F32 = 0, 1
 VIS_SCRATCH_BYTES = 64 << 20
 BLOCK_Q = 128
 KV_ALIGN = 64

@@ -200,8 +200,12 @@ class TextAttention:
         self.inv_freq = torch.from_numpy(rope_inv_freq(rope_theta, n_rot).copy()).to(self.device) \
             if n_rot else torch.zeros(1, dtype=torch.float32, device=self.device)
 
-    def planes(self, kvT):
-        """K plane [nkv][kvT][hd] (f16) and V^T plane [nkv][hd][kvT] (bf16)."""
+    def planes(self, kvT, fp32=False):
+        """K plane [nkv][kvT][hd] (f16) and V^T plane [nkv][hd][kvT] (bf16); with fp32 (the
+        FP32 mode, f32 qkv rows) K and V planes [nkv][kvT][hd], both f32."""
+        if fp32:
+            return (torch.empty((self.nkv, kvT, self.hd), dtype=torch.float32, device=self.device),
+                    torch.empty((self.nkv, kvT, self.hd), dtype=torch.float32, device=self.device))
         k = torch.empty((self.nkv, kvT, self.hd), dtype=torch.float16, device=self.device)
         vt = torch.empty((self.nkv, self.hd, kvT), dtype=torch.bfloat16, device=self.device)
         return k, vt
@@ -213,11 +217,14 @@ class TextAttention:
     def args(self, qkv, q_norm, k_norm, pos3, plan, out, k_plane, vt_plane, kvT,
              out_type=OUT_BF16, gate=True, ovf=None, f16_lim=65504.0, rope_cs=None, trace=None,
              schedule=True):
-        """The C argument block. schedule: hand the core a per-workgroup item split over the
-        device's CUs (clef_hip_attn_schedule), else it falls back to its static order."""
+        """The C argument block. qkv rows in bf16 select the tensor-unit path, f32 rows the FP32
+        path (qkv_type CLEF_HIP_QKV_F32, with f32 K and V planes). schedule: hand the bf16 core a
+        per-workgroup item split over the device's CUs (clef_hip_attn_schedule), else it falls
+        back to its static order; the FP32 core takes none."""
         T = plan.T
         dev = self.device
-        _check(qkv, "qkv", (T, qkv.shape[1] if qkv.dim() == 2 else -1), torch.bfloat16, dev)
+        fp32 = qkv.dtype == torch.float32
+        _check(qkv, "qkv", (T, qkv.shape[1] if qkv.dim() == 2 else -1), torch.float32 if fp32 else torch.bfloat16, dev)
         if qkv.shape[1] < self.row or qkv.shape[1] % 8:
             raise ValueError(f"qkv row {qkv.shape[1]} must be >= {self.row} and a multiple of 8")
         if (q_norm is None) != (k_norm is None):
@@ -227,8 +234,12 @@ class TextAttention:
             _check(k_norm, "k_norm", (self.hd,), torch.float32, dev)
         if self.n_rot:
             _check(pos3, "pos3", (T, 3), torch.int32, dev)
-        _check(k_plane, "k_plane", (self.nkv, kvT, self.hd), torch.float16, dev)
-        _check(vt_plane, "vt_plane", (self.nkv, self.hd, kvT), torch.bfloat16, dev)
+        if fp32:
+            _check(k_plane, "k_plane", (self.nkv, kvT, self.hd), torch.float32, dev)
+            _check(vt_plane, "v_plane", (self.nkv, kvT, self.hd), torch.float32, dev)
+        else:
+            _check(k_plane, "k_plane", (self.nkv, kvT, self.hd), torch.float16, dev)
+            _check(vt_plane, "vt_plane", (self.nkv, self.hd, kvT), torch.bfloat16, dev)
         if kvT < plan.kv_rows or kvT % 8:
             raise ValueError(f"kvT {kvT} must be >= {plan.kv_rows} and a multiple of 8")
         _check(out, "out", (T, self.nh * self.hd), {OUT_BF16: torch.bfloat16, OUT_F16: torch.float16,
@@ -255,8 +266,8 @@ class TextAttention:
         a.causal, a.gate = int(plan.causal), int(gate)
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
         a.trace = _ptr(trace)
-        a.seq_start, a.qkv_type = _ptr(plan.seq_start), _lib.QKV_BF16
-        if schedule and plan.n_blk:
+        a.seq_start, a.qkv_type = _ptr(plan.seq_start), _lib.QKV_F32 if fp32 else _lib.QKV_BF16
+        if schedule and plan.n_blk and not fp32:
             n_wg = _device_cus(dev)
             a.sched, a.n_wg = _ptr(plan.schedule(self.nh, self.nkv, n_wg)), n_wg
         return a
@@ -273,7 +284,7 @@ class TextAttention:
             out = torch.empty((plan.T, self.nh * self.hd), dtype=odt, device=self.device)
         if k_plane is None:
             kvT = plan.kvT
-            k_plane, vt_plane = self.planes(kvT)
+            k_plane, vt_plane = self.planes(kvT, fp32=qkv.dtype == torch.float32)
         elif kvT is None:
             kvT = k_plane.shape[1]
         if rope_cs is None and stage == "prefill" and self.n_rot:

@@ -12,6 +12,7 @@
 
 #include "attn_kernels.h"
 #include "attn_text.h"
+#include "attn_text_f32.h"
 #include "attn_vis.h"
 #include "attn_params.h"
 #include "clef_hip_attn.h"
@@ -23,7 +24,7 @@ static __device__ __align__(256) unsigned char scratch[CLEF_HIP_VIS_SCRATCH_BYTE
 
 namespace {
 
-constexpr int kVersion = 2;
+constexpr int kVersion = 3;
 constexpr int32_t kSchedMagic = 0x53434844;   // header word of a schedule ('SCHD')
 constexpr int kVisHD = 72;
 
@@ -60,15 +61,17 @@ bool rot_ok(int n_rot, int hd) {
 bool check_text(const clef_hip_attn_args *a, bool need_core, char *err, size_t errlen) {
     if (!a) return fail(err, errlen, "null attention arguments");
     if (a->hd != 256) return fail(err, errlen, "text attention supports hd 256 only (got %d)", a->hd);
-    if (a->qkv_type != CLEF_HIP_QKV_BF16)
-        return fail(err, errlen, "qkv_type %d not supported: the qkv rows must be bf16 (write them so from the QKV GEMM)", a->qkv_type);
+    if (a->qkv_type != CLEF_HIP_QKV_BF16 && a->qkv_type != CLEF_HIP_QKV_F32)
+        return fail(err, errlen, "qkv_type %d not supported: the qkv rows must be bf16 or f32", a->qkv_type);
+    const bool f32 = a->qkv_type == CLEF_HIP_QKV_F32;
     if (a->nh <= 0 || a->nkv <= 0 || a->nh % a->nkv) return fail(err, errlen, "bad head counts nh=%d nkv=%d", a->nh, a->nkv);
+    if (f32 && a->nh / a->nkv > 8) return fail(err, errlen, "FP32 mode takes at most 8 q heads per kv head (got %d)", a->nh / a->nkv);
     if (!rot_ok(a->n_rot, a->hd)) return fail(err, errlen, "unsupported n_rot %d", a->n_rot);
     if (a->T < 0 || a->n_blk < 0 || a->kv_rows < 0) return fail(err, errlen, "negative sizes");
     const long need_row = 2L * a->nh * a->hd + 2L * a->nkv * a->hd;
     if (a->row < need_row || a->row % 8) return fail(err, errlen, "qkv row %d must be >= %ld and a multiple of 8", a->row, need_row);
     if (a->kvT % 8 || a->kvT < a->kv_rows) return fail(err, errlen, "kvT %d must be a multiple of 8 and >= kv_rows %d", a->kvT, a->kv_rows);
-    if ((long)a->kvT * a->hd * 2 >= (1L << 32)) return fail(err, errlen, "kvT %d too large for 32-bit plane offsets", a->kvT);
+    if (!f32 && (long)a->kvT * a->hd * 2 >= (1L << 32)) return fail(err, errlen, "kvT %d too large for 32-bit plane offsets", a->kvT);
     if (!a->qkv || !aligned16(a->qkv)) return fail(err, errlen, "qkv must be a 16-byte aligned device pointer");
     if (!aligned16(a->k_norm) || !aligned16(a->q_norm)) return fail(err, errlen, "norm weights must be 16-byte aligned");
     if (!a->k_norm != !a->q_norm) return fail(err, errlen, "q_norm and k_norm must both be set or both be NULL");
@@ -161,6 +164,37 @@ bool vis_run(const clef_hip_vis_args *a, uint16_t *q_plane, uint16_t *k_plane, u
     p.causal = 0; p.gate = 0; p.out_type = a->out_type; p.out_ld = a->heads * kVisHD;
     hipLaunchKernelGGL(attn_vis_kernel, dim3((unsigned)(a->n_blk * a->heads)), dim3(64 * vis::WAVES), 0, (hipStream_t)stream, p);
     return launch_ok("attn_vis", err, errlen);
+}
+
+// The FP32 core: text32::SUB workgroups of nh / nkv waves per (plan block, kv head).
+template <int W>
+void launch_f32(const text32::Params &p, long grid, hipStream_t s) {
+    hipLaunchKernelGGL(text32::attn_text_f32_kernel<W>, dim3((unsigned)grid), dim3(64 * W), 0, s, p);
+}
+
+bool core_f32(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {
+    text32::Params p;
+    p.qkv = (const float *)a->qkv; p.q_norm = a->q_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
+    p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
+    p.k_plane = (const float *)a->k_plane; p.v_plane = (const float *)a->vt_plane; p.blocks = a->blocks;
+    p.out = a->out; p.ovf = a->ovf;
+    p.row = a->row; p.kvT = a->kvT; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot;
+    p.causal = a->causal ? 1 : 0; p.gate = a->gate ? 1 : 0; p.out_type = a->out_type;
+    p.eps = a->eps; p.scale = a->scale; p.f16_lim = f16_limit(a->f16_lim);
+    const long grid = (long)a->n_blk * text32::SUB * a->nkv;
+    if (grid > 0x7fffffffL) return fail(err, errlen, "grid too large");
+    hipStream_t s = (hipStream_t)stream;
+    switch (a->nh / a->nkv) {
+        case 1: launch_f32<1>(p, grid, s); break;
+        case 2: launch_f32<2>(p, grid, s); break;
+        case 3: launch_f32<3>(p, grid, s); break;
+        case 4: launch_f32<4>(p, grid, s); break;
+        case 5: launch_f32<5>(p, grid, s); break;
+        case 6: launch_f32<6>(p, grid, s); break;
+        case 7: launch_f32<7>(p, grid, s); break;
+        default: launch_f32<8>(p, grid, s); break;
+    }
+    return launch_ok("attn_text_f32", err, errlen);
 }
 
 }  // namespace
@@ -371,9 +405,20 @@ bool clef_hip_vis_positions(const int32_t *cu, int n_img, const int32_t *grid_w,
 bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {
     if (!check_text(a, false, err, errlen)) return false;
     if (a->T == 0 || a->kv_rows == 0) return true;
+    if (a->qkv_type == CLEF_HIP_QKV_F32) {
+        text32::PrepParams p;
+        p.qkv = (const float *)a->qkv; p.k_norm = a->k_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
+        p.kv_tok = a->kv_tok; p.k_plane = (float *)a->k_plane; p.v_plane = (float *)a->vt_plane;
+        p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
+        p.kv_rows = a->kv_rows; p.row = a->row; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
+        p.eps = a->eps;
+        const long groups = (long)a->kv_rows * a->nkv;
+        hipLaunchKernelGGL(text32::text_prep_kv_f32_kernel, dim3((unsigned)((groups + 7) / 8)), dim3(256), 0, (hipStream_t)stream, p);
+        return launch_ok("text_prep_kv_f32", err, errlen);
+    }
     PrepParams p;
-    p.qkv = a->qkv; p.k_norm = a->k_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
-    p.kv_tok = a->kv_tok; p.k_plane = a->k_plane; p.vt_plane = a->vt_plane;
+    p.qkv = (const uint16_t *)a->qkv; p.k_norm = a->k_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
+    p.kv_tok = a->kv_tok; p.k_plane = (uint16_t *)a->k_plane; p.vt_plane = (uint16_t *)a->vt_plane;
     p.kv_rows = a->kv_rows; p.row = a->row; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
     p.eps = a->eps; p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
     p.seq_start = a->seq_start; p.ovf = a->ovf; p.f16_lim = f16_limit(a->f16_lim);
@@ -385,11 +430,12 @@ bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err,
 bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {
     if (!check_text(a, true, err, errlen)) return false;
     if (a->n_blk == 0) return true;
+    if (a->qkv_type == CLEF_HIP_QKV_F32) return core_f32(a, stream, err, errlen);
     AttnParams p;
     memset(&p, 0, sizeof(p));
-    p.qkv = a->qkv; p.q_norm = a->q_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
+    p.qkv = (const uint16_t *)a->qkv; p.q_norm = a->q_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
     p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
-    p.k_plane = a->k_plane; p.vt_plane = a->vt_plane; p.blocks = a->blocks;
+    p.k_plane = (const uint16_t *)a->k_plane; p.vt_plane = (const uint16_t *)a->vt_plane; p.blocks = a->blocks;
     p.out = a->out; p.ovf = a->ovf;
     p.row = a->row; p.T = a->T; p.kvT = a->kvT; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot;
     p.eps = a->eps; p.scale_log2 = a->scale * 1.4426950408889634f;

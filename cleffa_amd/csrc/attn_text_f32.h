@@ -1,0 +1,396 @@
+// FP32 text attention for head dim 256 on CDNA4 (gfx950): the precision the reference's FP32
+// kernels give (metal/clef.metal:250-302 attn_prep, 316-654 attention / attention_fa /
+// attention_reuse / attention_prefetch_64), used for the per-record rerun after an f16 overflow
+// (clef.c:526-550) and with CLEF_ATTN_TU=0.
+//
+// Semantics (the reference's, per query row t of head h, kv head h / (nh / nkv)):
+//   q, k = RMSNorm(x) * w (w as given, already 1 + w), then partial rotary over dims [0, 64):
+//   pair (i, i + 32) turns by pos3[t][i % 3] * inv_freq[i]; V copied. S = (q . k) * scale over
+//   the record's keys up to the query's position, softmax with exp, O = P.V / l, times
+//   sigmoid(gate) (the second half of the head's row), written through act16 (bf16, or f16
+//   that saturates and flags the record) or as f32.
+//
+// Everything is FP32: the products run on v_mfma_f32_16x16x4f32 (FP32 operands, FP32
+// accumulation), the softmax in FP32 VALU. Key tiles start at the record's first key, so a
+// record's arithmetic does not depend on what is packed with it.
+//
+// Workgroup: one wave per q head of a GQA group (W = nh / nkv waves), all on the same 16 query
+// rows, so one 32-key K / V tile in LDS (64 KB, double buffered: 128 KB) serves the group.
+//   S^T = K . Q^T      A = 16 keys x 4 dims of K (LDS), B = the wave's Q (registers).
+//   O^T += V^T . P^T   A = 16 dims x 4 keys of V (LDS), B = P (registers).
+// Lane l = 16 g + r. S^T's A row r takes key 4(r % 4) + r / 4 of the 16-key subtile, so the four
+// scores a lane holds (accumulator rows 4g + v) are keys 4v + g: the B operand of the four 4-key
+// steps of the P.V product, with no shuffle. In S^T, lane (g, r) reads chunks 16g + j of its
+// key's K row (dims 64g + 4j + e); the K rows are padded to 1,040 bytes so those 16 rows fall in
+// distinct banks. In the P.V product, read j of lane r takes chunk 16j + r of its key's V row: a
+// read's 16 lanes cover 256 contiguous bytes. The A row r of dim tile 4j + e is then dim
+// 64j + 4r + e, and accumulator v of lane (g, r) in tile 4j + e holds dim 64j + 16g + 4v + e of
+// query row r. Every LDS read is a per-lane base register plus an immediate offset.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <utility>
+
+#include "clef_hip_attn.h"
+
+namespace clef_hip {
+namespace text32 {
+
+constexpr int HD = 256;
+constexpr int BQ = 16;                  // query rows per workgroup
+constexpr int SUB = 128 / BQ;           // workgroups per 128-row plan block
+constexpr int BK = 32;                  // keys per LDS tile
+constexpr int ROW = HD + 4;             // LDS floats per key row: 1,040 bytes, so the 16 rows
+                                        // one K read touches start 16 bytes apart in the banks
+constexpr int TILE = BK * ROW;          // floats per K or V tile (32.5 KB)
+constexpr int TB = TILE * 4;            // bytes per tile
+constexpr int RUN = 4;                  // K chunks read ahead of their products
+constexpr int NRUN = 16 / RUN;
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+struct PrepParams {
+    const float *qkv;           // [T][row]
+    const float *k_norm;        // [256] or NULL
+    const int32_t *pos3;
+    const float *inv_freq;      // [32]
+    const int32_t *kv_tok;      // pass row of each plane row, -1: not written
+    float *k_plane, *v_plane;   // [nkv][kvT][256]
+    float *rope_cs;             // [T][32][2] or NULL
+    int kv_rows, row, nh, nkv, n_rot, kvT;
+    float eps;
+};
+
+struct Params {
+    const float *qkv;
+    const float *q_norm;        // [256] or NULL
+    const int32_t *pos3;
+    const float *inv_freq;
+    const float *rope_cs;       // [T][32][2] written by the prep, or NULL
+    const float *k_plane, *v_plane;
+    const int32_t *blocks;      // the plan's 128-row blocks {q_row0, nq, q_pos0, k_row0, k_len, flag_row, ..}
+    void *out;
+    int32_t *ovf;
+    int row, kvT, nh, nkv, n_rot, causal, gate, out_type;
+    float eps, scale, f16_lim;
+};
+
+// The rotary angle's cos / sin in full FP32 precision (the reference: precise::cos / sin).
+__device__ __forceinline__ void rope_cs_f32(const int32_t *pos3, const float *inv_freq, int t, int i, float *c, float *s) {
+    const float ang = (float)pos3[3 * (size_t)t + i % 3] * inv_freq[i];
+    sincosf(ang, s, c);
+}
+
+// K / V prologue, FP32 planes: 32 lanes per (plane row, kv head); lane holds dims lane + 32 j,
+// so the rotary pair (i, i + 32), i < 32, sits in one lane. Plane rows with kv_tok -1 are left
+// as they are. Head 0's groups also store the rotary cos / sin of their pass row.
+__global__ __launch_bounds__(256) void text_prep_kv_f32_kernel(PrepParams p) {
+    const long item = (long)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int lane = threadIdx.x & 31;
+    if (item >= (long)p.kv_rows * p.nkv) return;
+    const int r = (int)(item / p.nkv), kh = (int)(item % p.nkv);
+    const int t = p.kv_tok[r];
+    if (t < 0) return;
+    const float *src = p.qkv + (size_t)t * p.row + (size_t)p.nh * 2 * HD + (size_t)kh * HD;
+    float x[8], v[8], ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        x[j] = src[lane + 32 * j];
+        v[j] = src[(size_t)p.nkv * HD + lane + 32 * j];
+        ss += x[j] * x[j];
+    }
+    if (p.k_norm) {
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 32);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+        for (int j = 0; j < 8; j++) x[j] = x[j] * inv * p.k_norm[lane + 32 * j];
+    }
+    if (p.n_rot) {
+        float c, s;
+        rope_cs_f32(p.pos3, p.inv_freq, t, lane, &c, &s);
+        const float x0 = x[0], x1 = x[1];
+        x[0] = x0 * c - x1 * s;
+        x[1] = x1 * c + x0 * s;
+        if (p.rope_cs && kh == 0) *(float2 *)(p.rope_cs + ((size_t)t * 32 + lane) * 2) = make_float2(c, s);
+    }
+    float *kd = p.k_plane + ((size_t)kh * p.kvT + r) * HD, *vd = p.v_plane + ((size_t)kh * p.kvT + r) * HD;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        kd[lane + 32 * j] = x[j];
+        vd[lane + 32 * j] = v[j];
+    }
+}
+
+// max over the four 16-lane rows of a wave (permlane swaps, VALU only); every lane gets it
+__device__ __forceinline__ float xrow_max(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float m = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
+template <int OFF>
+__device__ __forceinline__ f32x4 lds_read_f4(unsigned addr) {
+    f32x4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+    return r;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait_f4(f32x4 &r) {
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
+}
+
+template <typename F, int... I>
+__device__ __forceinline__ void sfor_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void sfor(F &&f) {
+    sfor_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// act16 of four values (metal/clef.metal:98-106): bf16, f16 saturating at +-65504 with the
+// record flag when |v| > lim or NaN, or f32.
+__device__ __forceinline__ void store_out4(void *out, size_t idx, f32x4 v, int out_type, float lim, int32_t *flag) {
+    if (out_type == CLEF_HIP_OUT_F32) {
+        *(f32x4 *)((float *)out + idx) = v;
+        return;
+    }
+    uint16_t h[4];
+    if (out_type == CLEF_HIP_OUT_BF16) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) h[e] = __builtin_bit_cast(uint16_t, (__bf16)v[e]);
+    } else {
+        bool bad = false;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float x = v[e];
+            if (!(fabsf(x) <= lim)) {
+                bad = true;
+                x = copysignf(65504.0f, x);
+            }
+            h[e] = __builtin_bit_cast(uint16_t, (_Float16)x);
+        }
+        if (bad && flag) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *(uint2 *)((uint16_t *)out + idx) = make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
+}
+
+// Grid: SUB workgroups per (plan block, kv head), block-major; wave w is q head kh * W + w.
+template <int W>
+__global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
+    __shared__ __attribute__((aligned(16))) float smem[4 * TILE];   // K0 | K1 | V0 | V1
+    const int kh = blockIdx.x % p.nkv, sb = blockIdx.x / p.nkv;
+    const int bi = sb / SUB, sub = sb % SUB;
+    const int32_t *blk = p.blocks + 8 * bi;
+    const int nq = min(BQ, blk[1] - BQ * sub);
+    if (nq <= 0) return;                                  // workgroup-uniform
+    const int q_row0 = blk[0] + BQ * sub, q_pos0 = blk[2] + BQ * sub, k_row0 = blk[3];
+    const int k_len = p.causal ? min(blk[4], q_pos0 + nq) : blk[4];
+    int32_t *flag = p.ovf ? p.ovf + blk[5] : nullptr;
+    const int n_tiles = (k_len + BK - 1) / BK;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int h = kh * W + wave;
+    const bool q_valid = r16 < nq;
+    const int qpos = q_pos0 + r16;
+    const int t = q_row0 + (q_valid ? r16 : 0);
+
+    // ---- tile fills: one 1 KB DMA group per key row; wave w fills rows w, w + W, ...
+    const float *kbase = p.k_plane + ((size_t)kh * p.kvT + k_row0) * HD;
+    const float *vbase = p.v_plane + ((size_t)kh * p.kvT + k_row0) * HD;
+    auto fill = [&](int kb, float *Ks, float *Vs) {
+        for (int r = wave; r < BK; r += W) {
+            const size_t off = (size_t)(kb + r) * HD + 4 * lane;
+            __builtin_amdgcn_global_load_lds((const void *)(kbase + off), (lds_void *)(Ks + r * ROW), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(vbase + off), (lds_void *)(Vs + r * ROW), 16, 0, 0);
+        }
+    };
+    // Rows past the keys (not written by this pass, possibly not finite) -> 0 in V, so that the
+    // zero probabilities of masked keys give exact zero products.
+    auto clear_tail = [&](int kb, float *Vs) {
+        if (kb + BK <= k_len) return;                     // workgroup-uniform
+        for (int r = wave; r < BK; r += W)
+            if (kb + r >= k_len) *(f32x4 *)(Vs + r * ROW + 4 * lane) = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    const unsigned lds0 = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) float *)smem;
+    // K: row 4(r16 % 4) + r16 / 4 of subtile 0, chunk 16g; V: row g, chunk r16 (buffer 0)
+    const unsigned ka = lds0 + (unsigned)(4 * (r16 & 3) + (r16 >> 2)) * ROW * 4u + 256u * g;
+    const unsigned va = lds0 + 2u * TB + (unsigned)g * ROW * 4u + 16u * r16;
+
+    if (n_tiles > 0) fill(0, smem, smem + 2 * TILE);
+
+    // ---- Q prologue: lane holds Q[row r16][64 g + c], normalised and rotated, FP32
+    float qf[64];
+    {
+        const f32x4 *qs = (const f32x4 *)(p.qkv + (size_t)t * p.row + (size_t)h * 2 * HD + 64 * g);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const f32x4 v = qs[j];
+            qf[4 * j] = v.x; qf[4 * j + 1] = v.y; qf[4 * j + 2] = v.z; qf[4 * j + 3] = v.w;
+        }
+        if (p.q_norm) {
+            float ss = 0.f;
+#pragma unroll
+            for (int c = 0; c < 64; c++) ss += qf[c] * qf[c];
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            const float inv = 1.0f / sqrtf(ss / (float)HD + p.eps);
+            const f32x4 *w = (const f32x4 *)(p.q_norm + 64 * g);
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const f32x4 wv = w[j];
+#pragma unroll
+                for (int e = 0; e < 4; e++) qf[4 * j + e] = qf[4 * j + e] * inv * wv[e];
+            }
+        }
+        if (p.n_rot && g == 0) {
+#pragma unroll
+            for (int i = 0; i < 32; i++) {
+                float c, s;
+                if (p.rope_cs) {
+                    const float2 cs = *(const float2 *)(p.rope_cs + ((size_t)t * 32 + i) * 2);
+                    c = cs.x; s = cs.y;
+                } else {
+                    rope_cs_f32(p.pos3, p.inv_freq, t, i, &c, &s);
+                }
+                const float x0 = qf[i], x1 = qf[i + 32];
+                qf[i] = x0 * c - x1 * s;
+                qf[i + 32] = x1 * c + x0 * s;
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    if (n_tiles > 0) clear_tail(0, smem + 2 * TILE);
+    __syncthreads();
+
+    f32x4 o[16];
+#pragma unroll
+    for (int n = 0; n < 16; n++) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+
+    auto tile = [&](const int ti, auto BUF) {
+        constexpr int buf = decltype(BUF)::value;
+        const int kb = ti * BK;
+        if (ti + 1 < n_tiles) fill(kb + BK, smem + (buf ^ 1) * TILE, smem + 2 * TILE + (buf ^ 1) * TILE);
+        // S^T: two 16-key subtiles, 64 four-dim steps each, K read in runs of RUN chunks
+        f32x4 s[2];
+        sfor<2>([&](auto U) {
+            constexpr int u = decltype(U)::value;
+            s[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+            sfor<NRUN>([&](auto H) {
+                constexpr int hh = decltype(H)::value;
+                f32x4 a[RUN];
+                sfor<RUN>([&](auto J) {
+                    constexpr int j = decltype(J)::value;
+                    a[j] = lds_read_f4<buf * TB + u * 16 * ROW * 4 + (RUN * hh + j) * 16>(ka);
+                });
+                sfor<RUN>([&](auto J) {
+                    constexpr int j = decltype(J)::value;
+                    lds_wait_f4<RUN - 1 - j>(a[j]);
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        s[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][e], qf[4 * (RUN * hh + j) + e], s[u], 0, 0, 0);
+                });
+            });
+        });
+        // V chunk j of step st = (u, v): key 16u + 4v + g, chunk 16j + r16 of its row
+        auto vread = [&](auto ST, auto J) {
+            constexpr int st = decltype(ST)::value, u = st >> 2, v = st & 3, j = decltype(J)::value;
+            return lds_read_f4<buf * TB + (16 * u + 4 * v) * ROW * 4 + 256 * j>(va);
+        };
+        f32x4 vb[4];   // step 0's chunks load while the softmax runs
+        sfor<4>([&](auto J) { vb[decltype(J)::value] = vread(std::integral_constant<int, 0>{}, J); });
+        // Online softmax. s[u][v] is the score of key kb + 16u + 4v + g for query row r16.
+        float x[2][4], mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int key = kb + 16 * u + 4 * v + g;
+                const bool ok = q_valid && key < k_len && (!p.causal || key <= qpos);
+                x[u][v] = ok ? s[u][v] * p.scale : -INFINITY;
+                mx = fmaxf(mx, x[u][v]);
+            }
+        const float mn = fmaxf(m_run, xrow_max(mx));
+        float pv[2][4];
+        float alpha = 1.f, rs = 0.f;
+        if (mn != -INFINITY) {
+            alpha = (m_run == -INFINITY) ? 0.f : expf(m_run - mn);
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    pv[u][v] = x[u][v] == -INFINITY ? 0.f : expf(x[u][v] - mn);
+                    rs += pv[u][v];
+                }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) pv[u][v] = 0.f;
+        }
+        m_run = mn;
+        l_run = l_run * alpha + rs;
+        const float alpha_o = alpha;
+        // O^T += V^T . P^T: 8 four-key steps (u, v), each 16 dim tiles. The V chunks roll
+        // through four registers: chunk j of the next step is read as soon as the current
+        // step's chunk j has fed its four products, so three reads are always in flight.
+#pragma unroll
+        for (int n = 0; n < 16; n++) o[n] *= alpha_o;
+        sfor<8>([&](auto S) {
+            constexpr int st = decltype(S)::value, u = st >> 2, v = st & 3;
+            const float b = pv[u][v];
+            sfor<4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                if constexpr (st + 1 < 8) lds_wait_f4<3>(vb[j]);
+                else lds_wait_f4<3 - j>(vb[j]);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    o[4 * j + e] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb[j][e], b, o[4 * j + e], 0, 0, 0);
+                if constexpr (st + 1 < 8) vb[j] = vread(std::integral_constant<int, st + 1>{}, J);
+            });
+        });
+        __builtin_amdgcn_s_waitcnt(0);
+        if (ti + 1 < n_tiles) clear_tail(kb + BK, smem + 2 * TILE + (buf ^ 1) * TILE);
+        __syncthreads();
+    };
+    for (int ti = 0; ti < n_tiles; ti += 2) {
+        tile(ti, std::integral_constant<int, 0>{});
+        if (ti + 1 < n_tiles) tile(ti + 1, std::integral_constant<int, 1>{});
+    }
+
+    // ---- epilogue: O = O^T / l, times sigmoid(gate). Accumulator n = 4j + e, entry v of lane
+    // (g, r16) is dim 64j + 16g + 4v + e of row r16.
+    float l_row = l_run;
+    l_row += __shfl_xor(l_row, 16);
+    l_row += __shfl_xor(l_row, 32);
+    if (q_valid) {
+        const float il = l_row > 0.f ? 1.0f / l_row : 0.f;
+        const float *grow = p.qkv + (size_t)t * p.row + (size_t)h * 2 * HD + HD;
+        const size_t obase = (size_t)t * p.nh * HD + (size_t)h * HD;
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int d = 64 * j + 16 * g + 4 * v;
+                f32x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; e++) w[e] = o[4 * j + e][v] * il;
+                if (p.gate) {
+                    const f32x4 gv = *(const f32x4 *)(grow + d);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) w[e] = w[e] * (1.0f / (1.0f + expf(-gv[e])));
+                }
+                store_out4(p.out, obase + d, w, p.out_type, p.f16_lim, flag);
+            }
+    }
+}
+
+}  // namespace text32
+}  // namespace clef_hip

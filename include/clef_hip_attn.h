@@ -90,7 +90,7 @@ typedef struct {
     int nh, nkv, hd, n_rot;   /* hd must be 256; n_rot 64 (Clef) or 0 */
     float eps, scale;         /* RMSNorm eps (1e-6), softmax scale (1/sqrt(hd)) */
     int T, row;               /* pass rows; qkv row stride in elements (multiple of 8) */
-    const uint16_t *qkv;      /* [T][row] bf16 */
+    const void *qkv;          /* [T][row]: bf16 (qkv_type CLEF_HIP_QKV_BF16) or f32 (CLEF_HIP_QKV_F32) */
     const float *q_norm;      /* [hd] f32, already 1 + w (tools/convert.py:7-8); NULL with k_norm: no norm */
     const float *k_norm;      /* [hd] f32, already 1 + w */
     const int32_t *pos3;      /* [T][3] */
@@ -99,8 +99,8 @@ typedef struct {
                                  rotary cos/sin there and core reads them (core alone with a table
                                  that prep_kv did not fill for this pass is undefined); NULL: core
                                  evaluates the angles itself */
-    uint16_t *k_plane;        /* [nkv][kvT][hd] */
-    uint16_t *vt_plane;       /* [nkv][hd][kvT] */
+    void *k_plane;            /* [nkv][kvT][hd]: f16 (bf16 mode) or f32 (FP32 mode) */
+    void *vt_plane;           /* bf16 mode: V^T [nkv][hd][kvT] bf16; FP32 mode: V [nkv][kvT][hd] f32 */
     int kvT;                  /* rows per head of the planes: >= plan kv_rows, multiple of 8 */
     const int32_t *blocks;    /* device copy of the plan's blocks */
     int n_blk;
@@ -133,13 +133,18 @@ typedef struct {
                                  seq_start, clef_engine.h:179), where prep_kv flags a key that
                                  leaves f16's range (see f16_lim); NULL: such keys are still
                                  saturated, but not flagged */
-    int qkv_type;             /* CLEF_HIP_QKV_BF16 (0), the only row type taken: the reference's
-                                 f32 rows (clef.metal:252) come from a QKV GEMM that writes bf16
-                                 here (clef_hip_gemm y_type CLEF_HIP_GEMM_Y_BF16); any other value
-                                 is rejected with an error */
+    int qkv_type;             /* CLEF_HIP_QKV_BF16 (0): the tensor-unit path (encode_attention_tu):
+                                 bf16 rows, f16 Q/K and bf16 P/V operands, f32 accumulation.
+                                 CLEF_HIP_QKV_F32 (1): the FP32 path (clef_metal.m:1330-1413,
+                                 attn_prep + attention_prefetch_64 and kin): f32 rows, f32 K and V
+                                 planes, FP32 products and softmax, for the per-record rerun after
+                                 an overflow (clef.c:526-550) and CLEF_ATTN_TU=0. In FP32 mode nh /
+                                 nkv must be at most 8, sched and trace are ignored, and only the
+                                 output (f16 out_type) can flag. Other values are rejected */
 } clef_hip_attn_args;
 
 #define CLEF_HIP_QKV_BF16 0
+#define CLEF_HIP_QKV_F32 1
 
 /* Static split of a text pass's work items (query block, q head) over n_wg workgroups of the
  * attention core, for clef_hip_attn_args.sched. No reference counterpart: the Metal backend

@@ -135,9 +135,9 @@ int main(int argc, char **argv) {
     if (!save(dir, "out_sched.bin", out, (size_t)T * NH * HD * 2)) return die("write", "out_sched.bin");
 
     /* f32 rows are refused before anything runs */
-    a.qkv_type = 1;
+    a.qkv_type = 2;
     if (clef_hip_attn_prefill(&a, NULL, err, sizeof err) || strncmp(err, "hip: ", 5))
-        return die("qkv_type", "an f32 qkv_type was not refused");
+        return die("qkv_type", "an unknown qkv_type was not refused");
     printf("abi_run ok: T %d, %d blocks, kvT %d\n", T, n_blk, kvT);
     return 0;
 }

@@ -53,7 +53,7 @@ def _args(**over):
     (dict(qkv=ctypes.c_void_p((1 << 20) + 2)), "qkv must be"),
     (dict(out_type=7), "out_type"),
     (dict(q_norm=None), "both"),
-    (dict(qkv_type=1), "qkv_type"),
+    (dict(qkv_type=2), "qkv_type"),
 ])
 def test_core_rejects_bad_arguments(over, msg):
     lib = _lib.load()
