@@ -113,7 +113,11 @@ def build_step(cfg, seed, fp32=False):
                    "fused q/k RMSNorm + rotary(64, theta 1e7) + sigmoid gate",
              "C2": "C2 single causal request: 16,384 tokens, 24/4 heads, hd 256, fused prologue/gate",
              "C3": "C3 prefix-cache continuation: 4 x (2,048 cached + 512 new), 16/4 heads, hd 256"}
-    info = dict(workload=names[cfg], tokens=T, pairs=plan.pairs(), hd=hd, nh=nh, bytes=nbytes,
+    # the attention kernel alone: Q and gate rows read once, each K / V plane row read once, O
+    # written once (the scope of roofline.traffic)
+    kv_rows = int(w["cu_seqlens_k"][-1]) if cfg == "C3" else T
+    core_bytes = T * 2 * nh * hd * esz + 2 * nkv * kv_rows * hd * (4 if fp32 else 2) + T * nh * hd * 2
+    info = dict(workload=names[cfg], tokens=T, pairs=plan.pairs(), hd=hd, nh=nh, bytes=nbytes, core_bytes=core_bytes,
                 lengths=[int(x) for x in np.diff(plan.cu_q)])
     return step, core, info, w
 
@@ -381,8 +385,9 @@ def main():
                            "frac": round(achieved / peak, 4),
                            "traffic": None if a.fp32 else measured_traffic(a.config),
                            "launch_ms": round(core_ms, 5),
-                           "algorithmic_bytes": info["bytes"],
-                           "hbm_frac_at_this_time": round(info["bytes"] / (core_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+                           "algorithmic_bytes": info["core_bytes"],
+                           "step_algorithmic_bytes": info["bytes"],
+                           "hbm_frac_at_this_time": round(info["core_bytes"] / (core_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
         # the same MFMA operand stream with random operands, measured now on this device: the
         # rate the part's power and clock allow (the nominal peak assumes 2.4 GHz)
         if not a.fp32:

@@ -174,6 +174,27 @@ def test_reference_packed_layout_bitwise(f16):
         assert_close(packed.float().cpu().numpy()[rows], oracle_text(w, rows=rows), what="reference packed")
 
 
+def test_many_one_token_records_bitwise():
+    """80 one-token records packed around longer ones (200, 70), so one-token records sit at every
+    row offset of a 128-row block and of a 64-key tile; each record equals its run alone bit for
+    bit (attention_bench.m:263-308 with more one-token records than one block holds)."""
+    _say("[invariance] 80 one-token records")
+    lengths = [1] * 40 + [200] + [1] * 40 + [70]
+    w = workloads.text_inputs(lengths, 8, 2, seed=29)
+    w.update(gate=True, theta=1e7)
+    cu = w["cu_seqlens"]
+    packed, _ = gpu_text(w)
+    packed_b = _bits(packed)
+    for r, n in enumerate(lengths):
+        a, b = int(cu[r]), int(cu[r + 1])
+        alone = dict(w, qkv=w["qkv"][a:b].clone(), pos3=w["pos3"][a:b].clone(),
+                     cu_seqlens=np.array([0, n], np.int32))
+        out, _ = gpu_text(alone)
+        assert torch.equal(_bits(out), packed_b[a:b]), f"record {r} (len {n}) bytes differ"
+    rows = np.arange(int(cu[-1]), dtype=np.int32)
+    assert_close(packed.float().cpu().numpy(), oracle_text(w, rows=rows), what="one-token records")
+
+
 @pytest.mark.parametrize("lengths", [[512] * 8, [1382] * 8, [4510, 346], [8072, 8072]],
                          ids=["8x512", "8x1382", "4510+346", "2x8072"])
 def test_reference_long_layouts(lengths):
