@@ -29,7 +29,23 @@ EXPORTS = (
     "clef_hip_omni_rope_table", "clef_hip_omni_prep", "clef_hip_omni_plan_max_blocks",
     "clef_hip_omni_plan", "clef_hip_omni_attention",
     "clef_hip_prefix_capacity", "clef_hip_prefix_plane_bytes", "clef_hip_prefix_copy",
+    "clef_hip_gguf_open", "clef_hip_gguf_close", "clef_hip_gguf_tensor_count", "clef_hip_gguf_tensor_at",
+    "clef_hip_gguf_find_tensor", "clef_hip_gguf_get_u32", "clef_hip_gguf_get_f32", "clef_hip_gguf_attn_config",
+    "clef_hip_gguf_attn_layer", "clef_hip_gguf_vis_layer",
 )
+
+GGML_F32, GGML_F16, GGML_BF16 = 0, 1, 30
+MAX_LAYERS = 128
+
+
+class GgufTensorInfo(ctypes.Structure):
+    _fields_ = [("n_dims", ctypes.c_uint32), ("type", ctypes.c_uint32), ("ne", ctypes.c_uint64 * 4),
+                ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64), ("data", c_void_p)]
+
+
+class AttnConfig(ctypes.Structure):
+    _fields_ = [("n_layer", c_int), ("H", c_int), ("nh", c_int), ("nkv", c_int), ("hd", c_int), ("n_rot", c_int),
+                ("eps", c_float), ("rope_theta", c_float), ("layer_full", c_int32 * MAX_LAYERS)]
 
 
 class AttnArgs(ctypes.Structure):
@@ -116,6 +132,28 @@ def load():
     lib.clef_hip_prefix_copy.argtypes = [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                                          c_void_p, c_char_p, c_size_t]
     lib.clef_hip_prefix_copy.restype = c_bool
+    lib.clef_hip_gguf_open.argtypes = [c_char_p, POINTER(c_void_p), c_char_p, c_size_t]
+    lib.clef_hip_gguf_open.restype = c_bool
+    lib.clef_hip_gguf_close.argtypes = [c_void_p]
+    lib.clef_hip_gguf_close.restype = None
+    lib.clef_hip_gguf_tensor_count.argtypes = [c_void_p]
+    lib.clef_hip_gguf_tensor_count.restype = c_int
+    lib.clef_hip_gguf_tensor_at.argtypes = [c_void_p, c_int, POINTER(GgufTensorInfo), c_char_p, c_size_t]
+    lib.clef_hip_gguf_tensor_at.restype = c_bool
+    lib.clef_hip_gguf_find_tensor.argtypes = [c_void_p, c_char_p, POINTER(GgufTensorInfo)]
+    lib.clef_hip_gguf_find_tensor.restype = c_bool
+    lib.clef_hip_gguf_get_u32.argtypes = [c_void_p, c_char_p, POINTER(ctypes.c_uint32)]
+    lib.clef_hip_gguf_get_u32.restype = c_bool
+    lib.clef_hip_gguf_get_f32.argtypes = [c_void_p, c_char_p, POINTER(c_float)]
+    lib.clef_hip_gguf_get_f32.restype = c_bool
+    lib.clef_hip_gguf_attn_config.argtypes = [c_void_p, POINTER(AttnConfig), c_char_p, c_size_t]
+    lib.clef_hip_gguf_attn_config.restype = c_bool
+    lib.clef_hip_gguf_attn_layer.argtypes = [c_void_p, POINTER(AttnConfig), c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                             c_void_p, c_char_p, c_size_t]
+    lib.clef_hip_gguf_attn_layer.restype = c_bool
+    lib.clef_hip_gguf_vis_layer.argtypes = [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                            c_char_p, c_size_t]
+    lib.clef_hip_gguf_vis_layer.restype = c_bool
     lib.clef_hip_attn_plan_max_blocks.argtypes = [c_int, c_int]
     lib.clef_hip_attn_plan_max_blocks.restype = c_int
     lib.clef_hip_attn_plan.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int, c_int,

@@ -7,12 +7,12 @@ ROOT = Path(__file__).resolve().parent
 REPO = ROOT.parent
 LIB = ROOT / "libclef_hip_attn.so"
 SOURCES = [ROOT / "csrc" / "attn_api.hip", ROOT / "csrc" / "prefix_cache.hip", ROOT / "csrc" / "omni_api.hip", ROOT / "csrc" / "records.cpp",
-           ROOT / "csrc" / "gemm_api.cpp"]
+           ROOT / "csrc" / "gemm_api.cpp", ROOT / "csrc" / "gguf_layer.cpp"]
 # the measurement utility bench.py uses, kept out of the engine-facing library
 BENCH_LIB = ROOT / "libclef_hip_bench.so"
 BENCH_SOURCES = [ROOT / "csrc" / "mfma_ceiling.hip"]
 DEPS = SOURCES + BENCH_SOURCES + [ROOT / "csrc" / "attn_kernels.h", ROOT / "csrc" / "attn_params.h", ROOT / "csrc" / "attn_text.h",
-                  ROOT / "csrc" / "attn_vis.h", ROOT / "csrc" / "omni_attn.h",
+                  ROOT / "csrc" / "attn_vis.h", ROOT / "csrc" / "omni_attn.h", ROOT / "csrc" / "attn_text_f32.h",
                   REPO / "include" / "clef_hip_attn.h"]
 
 

@@ -218,6 +218,54 @@ bool clef_hip_vis_attention_noalloc(const clef_hip_vis_args *a, void *stream, ch
 bool clef_hip_gemm(int T, int N, int K, const uint16_t *X, const uint16_t *W, void *Y, int y_type, int acc,
                    void *workspace, size_t ws_bytes, void *stream, char *err, size_t errlen);
 
+/* ---- The GEMMs' weights from the model file (clef_gguf.h / clef_gguf.c GGUF v3 reader; clef.c:27-59
+ * load_config, 180-256 bind_weights). Host-only except the copies: a read-only view over an
+ * mmap'd GGUF, every read bounds-checked (the file is untrusted), the attention geometry, and
+ * one layer's attention tensors copied into device buffers the caller owns. */
+#define CLEF_HIP_GGML_F32 0
+#define CLEF_HIP_GGML_F16 1
+#define CLEF_HIP_GGML_BF16 30
+#define CLEF_HIP_MAX_LAYERS 128   /* clef_engine.h:14 */
+typedef struct clef_hip_gguf clef_hip_gguf;
+typedef struct {
+    uint32_t n_dims, type;    /* 1..4; CLEF_HIP_GGML_* */
+    uint64_t ne[4];           /* ne[0] is the row length (fastest varying); unused dims are 1 */
+    uint64_t offset, nbytes;  /* absolute file offset and size of the data */
+    const void *data;         /* into the mapping, valid until clef_hip_gguf_close */
+} clef_hip_gguf_tensor_info;
+typedef struct {
+    int n_layer, H, nh, nkv, hd, n_rot;   /* clef.block_count, embedding_length, attention.head_count,
+                                             head_count_kv, key_length, rope.dimension_count */
+    float eps, rope_theta;                /* attention.layer_norm_rms_epsilon, rope.freq_base */
+    int32_t layer_full[CLEF_HIP_MAX_LAYERS];   /* clef.layer_types: 1 full attention, 0 DeltaNet */
+} clef_hip_attn_config;
+
+/* Fails on a missing file, a bad magic or version (3 only), counts the file cannot hold, nested
+ * arrays deeper than two, an alignment that is not a power of two, tensor types other than
+ * F32 / F16 / BF16, ranks outside 1..4 and tensor data outside the file. */
+bool clef_hip_gguf_open(const char *path, clef_hip_gguf **out, char *err, size_t errlen);
+void clef_hip_gguf_close(clef_hip_gguf *g);
+int clef_hip_gguf_tensor_count(const clef_hip_gguf *g);
+/* Tensor i of the table (file order) and its name, NUL-terminated into name[name_len]. */
+bool clef_hip_gguf_tensor_at(const clef_hip_gguf *g, int i, clef_hip_gguf_tensor_info *info, char *name, size_t name_len);
+bool clef_hip_gguf_find_tensor(const clef_hip_gguf *g, const char *name, clef_hip_gguf_tensor_info *info);
+bool clef_hip_gguf_get_u32(const clef_hip_gguf *g, const char *key, uint32_t *out);
+bool clef_hip_gguf_get_f32(const clef_hip_gguf *g, const char *key, float *out);
+/* general.architecture "clef", the keys above (u32 values in 1 .. 2^24), layer_types of
+ * n_layer entries each 0 or 1, nh a multiple of nkv. */
+bool clef_hip_gguf_attn_config(const clef_hip_gguf *g, clef_hip_attn_config *c, char *err, size_t errlen);
+/* Full-attention layer `layer`: blk.L.attn_qkv.weight BF16 [n_attn][H] (n_attn = 2 nh hd + 2 nkv hd,
+ * rows [q | gate] per head, then K, then V: the QKV GEMM's W), blk.L.attn_output.weight BF16
+ * [H][nh hd] (the o_proj's W), blk.L.attn_q_norm / attn_k_norm.weight F32 [hd] (already 1 + w).
+ * Each is checked for type and shape, then copied on `stream` into the given device buffer
+ * (NULL skips that tensor). */
+bool clef_hip_gguf_attn_layer(const clef_hip_gguf *g, const clef_hip_attn_config *c, int layer, uint16_t *w_qkv,
+                              uint16_t *w_o, float *q_norm, float *k_norm, void *stream, char *err, size_t errlen);
+/* Vision tower layer `layer` (clef.c:291-294): v.blk.L.attn_qkv.weight BF16 [3E][E] and .bias F32 [3E],
+ * v.blk.L.attn_out.weight BF16 [E][E] and .bias F32 [E], E = 72 heads. */
+bool clef_hip_gguf_vis_layer(const clef_hip_gguf *g, int layer, int heads, uint16_t *w_qkv, float *b_qkv,
+                             uint16_t *w_o, float *b_o, void *stream, char *err, size_t errlen);
+
 /* ---- Omni decoder attention (metal/clef.metal:2055-2319 omni_attn_prep / omni_attention, host
  * clef_metal_omni.m:200-245 clef_omni_encode_attention). FP32 operands, hd 128, causal within
  * each record, no gate; the output is accumulated in FP64 (the reference: FP32 hi/lo pairs).

@@ -16,8 +16,15 @@ LIB = HERE / "libattn_oracle.so"
 _lib = None
 
 
+REF_GGUF = HERE / "_ref" / "libclef_gguf_ref.so"
+REF_SRC = Path("/root/reference/clef_gguf.c")
+
+
 def build():
     subprocess.run(["make", "-B", "-C", str(HERE)], check=True, capture_output=True)
+    # the reference's own GGUF reader, compiled from its sources where they lie, when present
+    if REF_SRC.exists():
+        subprocess.run(["make", "-B", "-C", str(HERE), "ref"], check=True, capture_output=True)
     return LIB
 
 
