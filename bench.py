@@ -58,7 +58,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
     ap.add_argument("--profile-pass", action="store_true",
-                    help="for rocprofv3 --pmc: a 256 MiB device copy (counter calibration), then 3 eager "
+                    help="for rocprofv3 --pmc: a 256 MiB device copy and a 256 MiB elementwise pass "
+                         "(counter calibration), then 3 eager "
                          "steps; prints no JSON line")
     return ap.parse_args()
 
@@ -350,7 +351,8 @@ def main():
         src = torch.randn(CALIB_BYTES // 2, device="cuda").to(torch.bfloat16)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
-        dst.copy_(src)
+        dst.copy_(src)                     # the runtime's copy kernel
+        torch.mul(src, 1.0, out=dst)       # and an elementwise kernel with plain vector loads
         for _ in range(3):
             step()
         torch.cuda.synchronize()
