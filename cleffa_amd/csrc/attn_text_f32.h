@@ -180,12 +180,14 @@ __device__ __forceinline__ void store_out4(void *out, size_t idx, f32x4 v, int o
     *(uint2 *)((uint16_t *)out + idx) = make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
 }
 
-// Grid: SUB workgroups per (plan block, kv head), block-major; wave w is q head kh * W + w.
+// Grid: SUB workgroups per (plan block, kv head), block-major, each block's last rows first; wave w
+// is q head kh * W + w.
 template <int W>
 __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) float smem[4 * TILE];   // K0 | K1 | V0 | V1
     const int kh = blockIdx.x % p.nkv, sb = blockIdx.x / p.nkv;
-    const int bi = sb / SUB, sub = sb % SUB;
+    // the block's last 16 rows (its longest causal rows) first: blocks come longest first
+    const int bi = sb / SUB, sub = SUB - 1 - sb % SUB;
     const int32_t *blk = p.blocks + 8 * bi;
     const int nq = min(BQ, blk[1] - BQ * sub);
     if (nq <= 0) return;                                  // workgroup-uniform
@@ -278,25 +280,26 @@ __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
         constexpr int buf = decltype(BUF)::value;
         const int kb = ti * BK;
         if (ti + 1 < n_tiles) fill(kb + BK, smem + (buf ^ 1) * TILE, smem + 2 * TILE + (buf ^ 1) * TILE);
-        // S^T: two 16-key subtiles, 64 four-dim steps each, K read in runs of RUN chunks
-        f32x4 s[2];
-        sfor<2>([&](auto U) {
-            constexpr int u = decltype(U)::value;
-            s[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-            sfor<NRUN>([&](auto H) {
-                constexpr int hh = decltype(H)::value;
-                f32x4 a[RUN];
-                sfor<RUN>([&](auto J) {
-                    constexpr int j = decltype(J)::value;
-                    a[j] = lds_read_f4<buf * TB + u * 16 * ROW * 4 + (RUN * hh + j) * 16>(ka);
-                });
-                sfor<RUN>([&](auto J) {
-                    constexpr int j = decltype(J)::value;
-                    lds_wait_f4<RUN - 1 - j>(a[j]);
+        // S^T: two 16-key subtiles, 64 four-dim steps each, their products interleaved (two
+        // independent accumulator chains); K read in runs of RUN chunks per subtile
+        f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        sfor<NRUN>([&](auto H) {
+            constexpr int hh = decltype(H)::value;
+            f32x4 a[2][RUN];
+            sfor<RUN>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                a[0][j] = lds_read_f4<buf * TB + (RUN * hh + j) * 16>(ka);
+                a[1][j] = lds_read_f4<buf * TB + 16 * ROW * 4 + (RUN * hh + j) * 16>(ka);
+            });
+            sfor<RUN>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                lds_wait_f4<2 * (RUN - 1 - j) + 1>(a[0][j]);
+                lds_wait_f4<2 * (RUN - 1 - j)>(a[1][j]);
 #pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        s[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][e], qf[4 * (RUN * hh + j) + e], s[u], 0, 0, 0);
-                });
+                for (int e = 0; e < 4; e++) {
+                    s[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0][j][e], qf[4 * (RUN * hh + j) + e], s[0], 0, 0, 0);
+                    s[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1][j][e], qf[4 * (RUN * hh + j) + e], s[1], 0, 0, 0);
+                }
             });
         });
         // V chunk j of step st = (u, v): key 16u + 4v + g, chunk 16j + r16 of its row
