@@ -39,7 +39,7 @@ extern "C" {
 
 #define CLEF_HIP_OUT_BF16 0 /* bf16 (act16 with f16 off, metal/clef.metal:101) */
 #define CLEF_HIP_OUT_F16 1  /* f16; |v| > f16_lim or NaN saturates and flags (metal/clef.metal:98-106) */
-#define CLEF_HIP_OUT_F32 2  /* f32 (CLEF_VIS_F32 / FP32 kernels' unrounded output) */
+#define CLEF_HIP_OUT_F32 2  /* f32, unrounded: a store width only; FP32 arithmetic is qkv_type CLEF_HIP_QKV_F32 */
 
 #define CLEF_HIP_BLOCK_Q 128  /* query rows per block */
 #define CLEF_HIP_KV_ALIGN 64  /* kv row alignment of each record in a fresh pass */
