@@ -102,6 +102,34 @@ __device__ __forceinline__ void store_out8(void *out, size_t idx, const float *v
     }
 }
 
+// act16 of four consecutive output elements of one row (metal/clef.metal:98-106), as store_out8:
+// bf16, f16 saturating at +-65504 with the record flag when |v| > lim or NaN, or f32.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_out4(void *out, size_t idx, f32x4_t v, int out_type, float lim, int32_t *flag) {
+    if (out_type == CLEF_HIP_OUT_F32) {
+        *(f32x4_t *)((float *)out + idx) = v;
+        return;
+    }
+    uint16_t h[4];
+    if (out_type == CLEF_HIP_OUT_BF16) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) h[e] = __builtin_bit_cast(uint16_t, (__bf16)v[e]);
+    } else {
+        bool bad = false;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float x = v[e];
+            if (!(fabsf(x) <= lim)) {
+                bad = true;
+                x = copysignf(65504.0f, x);
+            }
+            h[e] = __builtin_bit_cast(uint16_t, (_Float16)x);
+        }
+        if (bad && flag) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *(uint2 *)((uint16_t *)out + idx) = make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 
 // ------------------------------------------------------------------------------------------

@@ -8,9 +8,10 @@
 // workgroups per CU.
 // The 72-dim contraction runs as three 32-dim chunks: Q holds zeros in dims 72..95, and the
 // K slots of those dims hold copies of real K chunks of the same row (finite), so they add 0.
-// O^T covers 96 rows: V^T rows 73..95 of both LDS buffers are zeroed once per workgroup and row
-// 72 is set to 1, so O^T row 72 accumulates the row sum of the rounded P (the softmax
-// denominator, rescaled with O) in the padding products the MFMAs run anyway.
+// O^T covers 80 rows in five 16-row tiles: tiles 0-3 hold dims 0-63 in the permuted row order
+// below, tile 4 rows 64-79 in natural order. V^T rows 73..79 of both LDS buffers are zeroed once
+// per workgroup and row 72 is set to 1, so O^T row 72 accumulates the row sum of the rounded P
+// (the softmax denominator, rescaled with O) in the padding products the MFMAs run anyway.
 // Q is pre-scaled by scale * log2 e and the S accumulators start at minus the row's running max,
 // so the products deliver the exponent of P directly; only when a tile moves the max (by more
 // than 8, rarely) is the difference subtracted and O rescaled.
@@ -23,12 +24,12 @@ constexpr int HD = 72;                 // head dim
 constexpr int ROWB = HD * 2;           // bytes per Q / K plane row (9 chunks of 16 bytes)
 constexpr int RCH = ROWB / 16;         // 16-byte chunks per plane row
 constexpr int NC = 3;                  // 32-dim chunks of the contraction (96 with padding)
-constexpr int NM = 6;                  // 16-row O^T tiles (96 rows)
-constexpr int HDV = 96;                // V^T rows in LDS
+constexpr int NM = 5;                  // 16-row O^T tiles (80 rows)
+constexpr int HDV = 80;                // V^T rows in LDS
 constexpr int BQ = 128, BK = 64, WAVES = 4, ROWS = 32;
 constexpr int KSLOTS = 16;             // 16-byte slots per K row in LDS (12 carry data)
 constexpr int KTILE = BK * KSLOTS * 8; // elements per K tile (16 KB)
-constexpr int VTILE = HDV * BK;        // elements per V^T tile (12 KB)
+constexpr int VTILE = HDV * BK;        // elements per V^T tile (10 KB)
 constexpr int LDS_ELEMS = 2 * KTILE + 2 * VTILE;
 }  // namespace vis
 
@@ -125,9 +126,13 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
     const int vx = text::v_swz(vrow);
     const unsigned va0 = vl + 2 * (vrow * BK + ((g ^ vx) * 8));
     const unsigned va1 = vl + 2 * (vrow * BK + (((4 + g) ^ vx) * 8));
+    // tile 4: row 64 + q16 (the swizzle of 64 + d is that of d)
+    const int nx = text::v_swz(q16);
+    const unsigned vn0 = vl + 2 * ((64 + q16) * BK + ((g ^ nx) * 8));
+    const unsigned vn1 = vl + 2 * ((64 + q16) * BK + (((4 + g) ^ nx) * 8));
 
     const int n_tiles = (k_len + BK - 1) / BK;
-    // V^T rows 72..95 of both buffers: row 72 all ones (bf16 1.0), the rest zero. A row is 64
+    // V^T rows 72..79 of both buffers: row 72 all ones (bf16 1.0), the rest zero. A row is 64
     // keys in 8 chunks whose order the swizzle permutes; the values are the same in every chunk.
     for (int i = tid; i < 2 * (HDV - HD) * BK / 8; i += 256) {
         const int b = i / ((HDV - HD) * BK / 8), r = i % ((HDV - HD) * BK / 8);
@@ -202,8 +207,12 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
             constexpr int PV = NM * 2;
             auto vread = [&](auto I) {   // step st = NM * kc + mt
                 constexpr int st = decltype(I)::value, mt = st % NM, kc = st / NM;
-                constexpr int off = buf * 2 * VTILE + (32 * (mt >> 1) + 4 * (mt & 1)) * BK * 2;
-                return lds_read16<off>(kc ? va1 : va0);
+                if constexpr (mt < 4) {
+                    constexpr int off = buf * 2 * VTILE + (32 * (mt >> 1) + 4 * (mt & 1)) * BK * 2;
+                    return lds_read16<off>(kc ? va1 : va0);
+                } else {
+                    return lds_read16<buf * 2 * VTILE>(kc ? vn1 : vn0);
+                }
             };
             bf16x8 vring[DEPTH];
             static_for<DEPTH>([&](auto I) { vring[decltype(I)::value] = vread(I); });
@@ -268,20 +277,20 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
         if (t + 1 < n_tiles) tile(t + 1, std::integral_constant<int, 1>{});
     }
 
-    // ---- Epilogue: O / l; lane (q16, g) holds dims 32u + 8g + [0, 8) (stored below dim 72)
+    // ---- Epilogue: O / l; lane (q16, g) holds dims 32u + 8g + [0, 8) of tiles 2u, 2u + 1 (u < 2)
+    // and dims 64 + 4g + [0, 4) of tile 4 (stored for g < 2)
     int32_t *flag = p.ovf ? p.ovf + flag_row : nullptr;
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
         const int my_q = wave * ROWS + 16 * hh + q16;
-        // the row sum sits in O^T row 72: tile 4, lane 16 + q16, element 0
-        const float l_row = __shfl(o[hh][4][0], 16 + q16);   // before the row-divergent exit
+        // the row sum sits in O^T row 72: tile 4, lane 32 + q16, element 0
+        const float l_row = __shfl(o[hh][4][0], 32 + q16);   // before the row-divergent exit
         if (my_q >= nq) continue;
         const float il = l_row > 0.f ? 1.f / l_row : 0.f;
         const size_t t = (size_t)q_row0 + my_q;
 #pragma unroll
-        for (int u = 0; u < NC; u++) {
+        for (int u = 0; u < 2; u++) {
             const int d0 = 32 * u + 8 * g;
-            if (d0 >= HD) continue;
             float v[8];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -290,6 +299,7 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
             }
             store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);
         }
+        if (g < 2) store_out4(p.out, t * p.out_ld + (size_t)h * HD + 64 + 4 * g, o[hh][4] * il, p.out_type, p.f16_lim, flag);
     }
 }
 
