@@ -212,7 +212,10 @@ bool clef_hip_vis_attention_noalloc(const clef_hip_vis_args *a, void *stream, ch
  * CLEF_HIP_GEMM_Y_BF16 writes bf16 (the qkv rows clef_hip_attn_prefill reads), CLEF_HIP_GEMM_Y_F32
  * f32; acc != 0 adds into an f32 Y (the residual stream). workspace (may be NULL with ws_bytes 0)
  * is device scratch the algorithm may use. Runs on hipBLASLt; the algorithm of each shape is
- * chosen on its first call. */
+ * chosen on its first call. For acc == 0 that call times up to 16 of hipBLASLt's candidates on
+ * the caller's operands and stream (Y is overwritten by each and finally by the chosen one), so
+ * it waits for the stream once. An accumulating call, or one under graph capture, takes
+ * hipBLASLt's first candidate; a choice made under capture is timed at the next uncaptured call. */
 #define CLEF_HIP_GEMM_Y_F32 0
 #define CLEF_HIP_GEMM_Y_BF16 1
 bool clef_hip_gemm(int T, int N, int K, const uint16_t *X, const uint16_t *W, void *Y, int y_type, int acc,

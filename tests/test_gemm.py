@@ -77,3 +77,39 @@ def test_gemm_accumulates_into_residual():
     bound = _bound(X, W) + 2.0 ** -23 * want.abs()
     assert ((Y.double() - want).abs() <= bound).all()
     assert ((Y2.double() - want).abs() <= bound).all()
+
+
+@pytest.mark.gpu
+def test_gemm_first_call_captured_then_timed():
+    """A shape first met under graph capture takes hipBLASLt's first candidate (nothing can be
+    timed); the next uncaptured call times the candidates and replaces it; both graphs replay
+    correctly, each replay checked against the float64 product with eager work in between."""
+    print("[gemm] capture, then timed", flush=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    T, N, K = 257, 1536, 1024   # a shape no other test uses
+    X = torch.randn(T, K, generator=g, device="cuda").bfloat16()
+    W = (0.05 * torch.randn(N, K, generator=g, device="cuda")).bfloat16()
+    ws = torch.empty(32 << 20, dtype=torch.uint8, device="cuda")
+    ref, bound = _ref(X, W), _bound(X, W)
+    Yb = torch.empty(T, N, device="cuda", dtype=torch.bfloat16)
+    ulp = torch.where(ref.abs() > 0, 2.0 ** (torch.floor(torch.log2(ref.abs())) - 7), torch.zeros_like(ref))
+    graphs = []
+    for rnd in range(2):
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            gemm(X, W, Y=Yb, out="bf16", workspace=ws)
+        graphs.append(gr)
+        if rnd == 0:   # an uncaptured call: times the candidates, replaces the captured choice
+            Yb.zero_()
+            gemm(X, W, Y=Yb, out="bf16", workspace=ws)
+            torch.cuda.synchronize()
+            assert ((Yb.double() - ref).abs() <= bound + ulp).all(), "timed call"
+    for gr in graphs:
+        for _ in range(3):
+            Yb.fill_(float("nan"))
+            gr.replay()
+            torch.cuda.synchronize()
+            assert ((Yb.double() - ref).abs() <= bound + ulp).all(), "graph replay"
+            torch.mm(X.float(), W.float().T)   # eager work between replays
