@@ -168,13 +168,37 @@ __global__ __launch_bounds__(16 * kPrepRows) void text_prep_kv_kernel(PrepParams
     const int t = (r0 + rr < p.kv_rows) ? p.kv_tok[r0 + rr] : -1;
     if (k == 0) trow[rr] = t;
     if (!__syncthreads_or(t >= 0)) return;       // no row of this tile belongs to the pass
-    // global loads first
+    // Global loads first, all in flight together: the row's K and V chunks, the positions and
+    // frequencies of this thread's rotary-table entries, the k_norm weights. The loads are
+    // unconditional (a row the pass does not own reads pass row 0) and the values selected after:
+    // a load under a condition becomes a branch, and the compiler waits for it at the join.
     const uint16_t *src = p.qkv + (size_t)(t >= 0 ? t : 0) * p.row + (size_t)p.nh * 2 * HD + (size_t)kh * HD + 16 * k;
     u32x4 kw[2], vw[2];
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-        kw[h] = t >= 0 ? *(const u32x4 *)(src + 8 * h) : u32x4{0, 0, 0, 0};
-        vw[h] = t >= 0 ? *(const u32x4 *)(src + (size_t)p.nkv * HD + 8 * h) : u32x4{0, 0, 0, 0};
+        kw[h] = *(const u32x4 *)(src + 8 * h);
+        vw[h] = *(const u32x4 *)(src + (size_t)p.nkv * HD + 8 * h);
+    }
+    // rotary table of the tile: ROWS x 32 pairs, pair i turns by axis i % 3; entry idx = tid + NT j
+    constexpr int TJ = ROWS * 32 / NT;
+    int rtt[TJ], rpos[TJ];
+    float rfreq[TJ];
+    if (half_rot) {
+#pragma unroll
+        for (int j = 0; j < TJ; j++) {
+            const int idx = tid + NT * j, row = idx >> 5, i = idx & 31;
+            rtt[j] = trow[row];
+            rpos[j] = p.pos3[3 * (size_t)(rtt[j] >= 0 ? rtt[j] : 0) + i % 3];
+            rfreq[j] = p.inv_freq[i];
+        }
+    }
+    float wn[16];
+    if (p.k_norm) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 w4 = *(const float4 *)(p.k_norm + 16 * k + 4 * q);
+            wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
+        }
     }
     // A non-finite V element (bf16 exponent all ones) saturates to +-65536 (bf16's rounding of
     // 65504) and flags the record, as split16 does for the reference's f16 V plane
@@ -184,33 +208,24 @@ __global__ __launch_bounds__(16 * kPrepRows) void text_prep_kv_kernel(PrepParams
     for (int h = 0; h < 2; h++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            unsigned w = vw[h][j];
+            kw[h][j] = t >= 0 ? kw[h][j] : 0u;
+            unsigned w = t >= 0 ? vw[h][j] : 0u;
             const bool lo_bad = (w & 0x7f80u) == 0x7f80u, hi_bad = (w & 0x7f800000u) == 0x7f800000u;
             if (lo_bad) w = (w & 0xffff8000u) | 0x4780u;
             if (hi_bad) w = (w & 0x8000ffffu) | 0x47800000u;
             bad |= lo_bad | hi_bad;
             vw[h][j] = w;
         }
-    float wn[16];
-    if (p.k_norm) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 w4 = *(const float4 *)(p.k_norm + 16 * k + 4 * q);
-            wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
-        }
-    }
     if (half_rot) {
-        // rotary table of the tile: ROWS x 32 pairs, pair i turns by axis i % 3
 #pragma unroll
-        for (int j = 0; j < ROWS * 32 / NT; j++) {
+        for (int j = 0; j < TJ; j++) {
             const int idx = tid + NT * j, row = idx >> 5, i = idx & 31;
-            const int tt = trow[row];
-            if (tt >= 0) {
-                const float ang = (float)p.pos3[3 * (size_t)tt + i % 3] * p.inv_freq[i];
+            if (rtt[j] >= 0) {
+                const float ang = (float)rpos[j] * rfreq[j];
                 float sn, cn;
                 rope_sincos(ang, &sn, &cn);
                 csl[row][i] = make_float2(cn, sn);
-                if (p.rope_cs && kh == 0) *(float2 *)(p.rope_cs + (size_t)tt * 2 * half_rot + 2 * i) = make_float2(cn, sn);
+                if (p.rope_cs && kh == 0) *(float2 *)(p.rope_cs + (size_t)rtt[j] * 2 * half_rot + 2 * i) = make_float2(cn, sn);
             }
         }
     }
