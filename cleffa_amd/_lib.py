@@ -106,7 +106,7 @@ def load():
     lib.clef_hip_attn_wave_size.restype = c_int
     lib.clef_hip_attn_init.argtypes = [c_char_p, c_size_t]
     lib.clef_hip_attn_init.restype = c_bool
-    lib.clef_hip_record_positions.argtypes = [c_int, POINTER(c_int32), POINTER(c_int32), POINTER(c_int32),
+    lib.clef_hip_record_positions.argtypes = [c_int, POINTER(c_int32), POINTER(c_int32), POINTER(c_int32), POINTER(c_int32),
                                               c_int, c_int, POINTER(c_int32), c_char_p, c_size_t]
     lib.clef_hip_record_positions.restype = c_bool
     lib.clef_hip_pack_batch.argtypes = [POINTER(c_int32), ctypes.c_void_p, c_int, c_int, ctypes.c_long, POINTER(c_int32)]

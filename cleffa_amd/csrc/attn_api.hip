@@ -24,7 +24,7 @@ static __device__ __align__(256) unsigned char scratch[CLEF_HIP_VIS_SCRATCH_BYTE
 
 namespace {
 
-constexpr int kVersion = 3;
+constexpr int kVersion = 4;
 constexpr int32_t kSchedMagic = 0x53434844;   // header word of a schedule ('SCHD')
 constexpr int kVisHD = 72;
 

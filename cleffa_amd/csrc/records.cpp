@@ -23,13 +23,20 @@ bool rfail(char *err, size_t errlen, const char *fmt, ...) {
 
 extern "C" {
 
-// clef_record.c:938-962 (clef_record_positions): text tokens take (p, p, p) with p counting up
-// from 0; a vision span covers the merged grid (grid_h / merge) x (grid_w / merge) row-major,
-// token (y, x) taking (p, p + y, p + x), after which p advances by the larger merged side.
-bool clef_hip_record_positions(int T, const int32_t *span_start, const int32_t *span_grid_h,
-                               const int32_t *span_grid_w, int n_spans, int merge, int32_t *pos3,
-                               char *err, size_t errlen) {
-    if (T < 0 || n_spans < 0 || merge <= 0 || (T && !pos3) || (n_spans && (!span_start || !span_grid_h || !span_grid_w)))
+// clef_record.c:938-962 (clef_record_positions): a record that carries its own positions
+// (pos3_given, the reference's r->pos3, 939-942) has them copied; otherwise text tokens take
+// (p, p, p) with p counting up from 0, and a vision span covers the merged grid
+// (grid_h / merge) x (grid_w / merge) row-major, token (y, x) taking (p, p + y, p + x), after
+// which p advances by the larger merged side.
+bool clef_hip_record_positions(int T, const int32_t *pos3_given, const int32_t *span_start,
+                               const int32_t *span_grid_h, const int32_t *span_grid_w, int n_spans, int merge,
+                               int32_t *pos3, char *err, size_t errlen) {
+    if (T < 0 || (T && !pos3)) return rfail(err, errlen, "bad record position arguments");
+    if (pos3_given) {
+        if (T) memmove(pos3, pos3_given, (size_t)T * 3 * sizeof(int32_t));
+        return true;
+    }
+    if (n_spans < 0 || merge <= 0 || (n_spans && (!span_start || !span_grid_h || !span_grid_w)))
         return rfail(err, errlen, "bad record position arguments");
     int32_t cur = 0;
     int t = 0, next = 0;

@@ -12,16 +12,21 @@ def _i32p(a):
     return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
 
 
-def record_positions(T, spans=(), merge=2):
+def record_positions(T, spans=(), merge=2, given=None):
     """pos3 [T][3] int32 of one record. spans: (token start, grid_h, grid_w) per vision span in
-    token order (grid sizes in patches, before the merge)."""
+    token order (grid sizes in patches, before the merge). given: the record's own [T][3]
+    positions (an Omni record's), copied as they are."""
     lib = _lib.load()
     sp = np.asarray(spans, dtype=np.int32).reshape(-1, 3)
     start, gh, gw = (np.ascontiguousarray(sp[:, i]) for i in range(3))
     pos3 = np.zeros((max(T, 1), 3), dtype=np.int32)
+    if given is not None:
+        given = np.ascontiguousarray(given, dtype=np.int32)
+        if given.shape != (T, 3):
+            raise ValueError(f"given positions have shape {given.shape}, expected ({T}, 3)")
     err = ctypes.create_string_buffer(256)
-    ok = lib.clef_hip_record_positions(int(T), _i32p(start), _i32p(gh), _i32p(gw), len(sp), int(merge),
-                                       _i32p(pos3), err, len(err))
+    ok = lib.clef_hip_record_positions(int(T), None if given is None else _i32p(given), _i32p(start), _i32p(gh),
+                                       _i32p(gw), len(sp), int(merge), _i32p(pos3), err, len(err))
     _lib.check(ok, err)
     return pos3[:T]
 

@@ -343,14 +343,17 @@ bool clef_hip_prefix_copy(const uint16_t *k_src, const uint16_t *vt_src, int src
 
 /* Host-only producers of the path's inputs. */
 
-/* M-RoPE positions pos3 [T][3] of one record (clef_record.c:938-962, clef_record_positions):
- * text tokens take (p, p, p) with p counting up from 0; vision span i (an image, or one frame of
- * a video) starts at token span_start[i] and covers its merged grid, (span_grid_h[i] / merge) x
- * (span_grid_w[i] / merge) tokens row-major, token (y, x) taking (p, p + y, p + x), after which
- * p advances by the larger merged side. Spans in token order, not overlapping. */
-bool clef_hip_record_positions(int T, const int32_t *span_start, const int32_t *span_grid_h,
-                               const int32_t *span_grid_w, int n_spans, int merge, int32_t *pos3,
-                               char *err, size_t errlen);
+/* M-RoPE positions pos3 [T][3] of one record (clef_record.c:938-962, clef_record_positions).
+ * A record that carries its own positions (the reference's r->pos3, Omni records) passes them as
+ * pos3_given [T][3]: they are copied and the span arguments are not read. Otherwise (pos3_given
+ * NULL) text tokens take (p, p, p) with p counting up from 0; vision span i (an image, or one
+ * frame of a video) starts at token span_start[i] and covers its merged grid,
+ * (span_grid_h[i] / merge) x (span_grid_w[i] / merge) tokens row-major, token (y, x) taking
+ * (p, p + y, p + x), after which p advances by the larger merged side. Spans in token order, not
+ * overlapping. */
+bool clef_hip_record_positions(int T, const int32_t *pos3_given, const int32_t *span_start,
+                               const int32_t *span_grid_h, const int32_t *span_grid_w, int n_spans, int merge,
+                               int32_t *pos3, char *err, size_t errlen);
 
 /* Micro-batch packing of the server's queue (clef_server.c:311-327): first in, first out; the
  * head is always taken, then requests while fewer than max_batch are taken and the tokens stay

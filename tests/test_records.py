@@ -81,3 +81,14 @@ def test_adjacent_spans_stay_separate():
     # positions 0 and 1 (transformers would read them as one 1x2 run of vision tokens).
     np.testing.assert_array_equal(record_positions(3, [(0, 2, 2), (1, 2, 2)]),
                                   [[0, 0, 0], [1, 1, 1], [2, 2, 2]])
+
+
+def test_given_positions_are_copied():
+    """A record that carries its own positions (clef_record.c:939-942, r->pos3: an Omni record's
+    precomputed [T][3]) gets them back as they are; spans are not read."""
+    rng = np.random.default_rng(3)
+    given = rng.integers(-5, 1000, size=(7, 3)).astype(np.int32)
+    np.testing.assert_array_equal(record_positions(7, [(0, 2, 2)], given=given), given)
+    np.testing.assert_array_equal(record_positions(0, given=np.zeros((0, 3), np.int32)), np.zeros((0, 3), np.int32))
+    with pytest.raises(ValueError, match="expected"):
+        record_positions(7, given=given[:5])
