@@ -59,17 +59,18 @@ std::mutex mu;
 std::map<int, hipblasLtHandle_t> handles;
 std::map<Key, Plan> plans;
 
-// Row-major Y[T][N] = X[T][K] . W[N][K]^T is, column-major, Y^T (N x T) = W^T' (N x K) . X^T (K x T)
-// with W read as a K x N column-major matrix, transposed (A), and X as K x T, not transposed (B).
+// Candidates timed on a shape's first call, and runs per candidate (after one warm-up): the one
+// with the shortest median run is kept.
 constexpr int kTune = 16;
-
-// The algorithm with the shortest median time over kTuneRuns runs, after one warm-up each.
 constexpr int kTuneRuns = 5;
 bool tune(hipblasLtHandle_t h, Plan *p, const hipblasLtMatmulHeuristicResult_t *res, int found, const uint16_t *X,
           const uint16_t *W, void *Y, void *workspace, size_t ws_bytes, hipStream_t stream, char *err, size_t errlen) {
     hipEvent_t ev[kTuneRuns + 1];
     for (int i = 0; i <= kTuneRuns; i++)
-        if (hipEventCreate(&ev[i]) != hipSuccess) return fail(err, errlen, "hipEventCreate failed");
+        if (hipEventCreate(&ev[i]) != hipSuccess) {
+            while (i-- > 0) (void)hipEventDestroy(ev[i]);
+            return fail(err, errlen, "hipEventCreate failed");
+        }
     const float alpha = 1.f, beta = 0.f;
     float best = 0.f;
     int best_i = -1;
@@ -87,7 +88,8 @@ bool tune(hipblasLtHandle_t h, Plan *p, const hipblasLtMatmulHeuristicResult_t *
             continue;
         }
         float t[kTuneRuns];
-        for (int r = 0; r < kTuneRuns; r++) hipEventElapsedTime(&t[r], ev[r], ev[r + 1]);
+        for (int r = 0; r < kTuneRuns && ok; r++) ok = hipEventElapsedTime(&t[r], ev[r], ev[r + 1]) == hipSuccess;
+        if (!ok) continue;
         for (int a = 1; a < kTuneRuns; a++)   // insertion sort, for the median
             for (int b = a; b > 0 && t[b] < t[b - 1]; b--) std::swap(t[b], t[b - 1]);
         const float med = t[kTuneRuns / 2];
