@@ -197,6 +197,9 @@ bool core_f32(const clef_hip_attn_args *a, void *stream, char *err, size_t errle
     return launch_ok("attn_text_f32", err, errlen);
 }
 
+// a pass with fewer (block, head) items than workgroups splits its blocks of more than 64 rows
+bool sched_splits(int n_blk, int nh, int n_wg) { return (long)n_blk * nh < n_wg; }
+
 }  // namespace
 
 extern "C" {
@@ -221,29 +224,45 @@ bool clef_hip_attn_init(char *err, size_t errlen) {
 
 int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg) {
     if (n_blk < 0 || nh <= 0 || n_wg <= 0) return 0;
-    return 4 + n_wg + 1 + n_blk * nh;
+    const long items = (long)n_blk * nh * (sched_splits(n_blk, nh, n_wg) ? 2 : 1);
+    return items + 5 + n_wg > 0x7fffffffL ? 0 : (int)(4 + n_wg + 1 + items);
 }
 
 bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,
                             int32_t *sched, int max_sched, char *err, size_t errlen) {
     if ((n_blk && !blocks) || !sched || n_blk < 0 || nh <= 0 || nkv <= 0 || nh % nkv || n_wg <= 0)
         return fail(err, errlen, "bad schedule arguments");
-    const long need = 4L + n_wg + 1 + (long)n_blk * nh;
+    if ((long)n_blk * nh >= (1L << 28)) return fail(err, errlen, "too many items for a schedule");
+    const bool split = sched_splits(n_blk, nh, n_wg);
+    const long need = 4L + n_wg + 1 + (long)n_blk * nh * (split ? 2 : 1);
     if (need > max_sched) return fail(err, errlen, "schedule needs %ld entries, room for %d", need, max_sched);
     // cost of an item in 64-key tiles: its tiles plus the prologue / epilogue (Q rows, gate,
-    // output stores), measured at about three tiles' time per item
+    // output stores), measured at about three tiles' time per item. A first half's keys end at
+    // its last row when the pass is causal (the estimate assumes it is).
     constexpr int kFixed = 3;
     const int xh = (nh % 8 == 0 && ((nh / nkv) % (nh / 8) == 0 || (nh / 8) % (nh / nkv) == 0)) ? nh / 8 : 0;
     const int groups = (xh && n_wg % 8 == 0) ? 8 : 1;
-    auto cost_of = [&](int item) { return (blocks[8 * (item / nh) + 4] + 63) / 64 + kFixed; };
+    auto cost_of = [&](int item) {
+        const int32_t *e = blocks + 8 * ((item & ((1 << 28) - 1)) / nh);
+        const int k_len = (item >> 28) == 1 ? std::min(e[4], e[2] + 64) : e[4];
+        return (k_len + 63) / 64 + kFixed;
+    };
     std::vector<std::vector<int>> lists(n_wg);
     std::vector<long> load(n_wg, 0);
     for (int x = 0; x < groups; x++) {
         // items of this XCD group, longest first (the plan's blocks already are)
         std::vector<std::pair<int, int>> its;   // (cost, item)
         for (int bi = 0; bi < n_blk; bi++) {
-            for (int h = 0; h < nh; h++)
-                if (groups == 1 || h / xh == x) its.push_back({cost_of(bi * nh + h), bi * nh + h});
+            for (int h = 0; h < nh; h++) {
+                if (groups != 1 && h / xh != x) continue;
+                const int it = bi * nh + h;
+                if (split && blocks[8 * bi + 1] > 64) {   // the block's rows 0-63 and 64-127
+                    its.push_back({cost_of(it | (1 << 28)), it | (1 << 28)});
+                    its.push_back({cost_of(it | (2 << 28)), it | (2 << 28)});
+                } else {
+                    its.push_back({cost_of(it), it});
+                }
+            }
         }
         std::stable_sort(its.begin(), its.end(), [](const std::pair<int, int> &u, const std::pair<int, int> &v) { return u.first > v.first; });
         for (const auto &it : its) {

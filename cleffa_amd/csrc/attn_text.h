@@ -113,6 +113,12 @@ __device__ __forceinline__ int sload(const int32_t *ptr) {
     asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(ptr) : "memory");
     return v;
 }
+// A schedule item: block * nh + head in bits 0-27, and in bits 28-29 the rows of the block it
+// covers: 0 all, 1 rows 0-63, 2 rows 64-127 (a pass with fewer items than workgroups splits its
+// blocks so that every workgroup has work). A row's arithmetic does not depend on the split:
+// each 16-row wave runs the key tiles up to its own last row, from the record's first key.
+constexpr int kItemBits = 28;
+__device__ __forceinline__ int item_base(int it) { return it & ((1 << kItemBits) - 1); }
 struct ItemList {
     int n_items, per_x, gx, xh, nh, s0, s1;
     const int32_t *list;
@@ -132,12 +138,12 @@ struct ItemList {
             list = offs + gridDim.x + 1;
         }
     }
-    // the k-th item of this workgroup as block * nh + head, or -1
+    // the k-th item of this workgroup (block * nh + head, with the rows code above), or -1
     __device__ __forceinline__ int get(int k) const {
         if (list) {
             if (s0 + k >= s1) return -1;
             const int it = sload(list + s0 + k);
-            return (it >= 0 && it < n_items) ? it : -1;   // never an item outside the plan
+            return (it >= 0 && (it >> kItemBits) <= 2 && item_base(it) < n_items) ? it : -1;   // never an item outside the plan
         }
         if (xh && gx && ((int)gridDim.x & 7) == 0) {
             const int x = blockIdx.x & 7, wl = blockIdx.x >> 3;
@@ -211,9 +217,16 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     // once the kernel has stored anything, and those would wait behind the in-flight tile fills.
     auto decode_from = [&](const i32x8 &e, int it) {
         Item s;
-        const int bi = it / p.nh;
-        s.h = it - bi * p.nh;
+        const int base = item_base(it), half = it >> kItemBits;
+        const int bi = base / p.nh;
+        s.h = base - bi * p.nh;
         s.q_row0 = e[0]; s.nq = e[1]; s.q_pos0 = e[2]; s.k_row0 = e[3]; s.k_len = e[4];
+        if (half == 1) {          // rows 0-63: a causal half sees keys up to its own last row
+            s.nq = min(s.nq, 64);
+            if (p.causal) s.k_len = min(s.k_len, s.q_pos0 + s.nq);
+        } else if (half == 2) {   // rows 64-127
+            s.q_row0 += 64; s.q_pos0 += 64; s.nq -= 64;
+        }
         s.flag_row = e[5];
         s.kh = s.h / (p.nh / p.nkv);
         s.n_tiles = (s.k_len + BK - 1) / BK;
@@ -223,7 +236,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     };
     auto decode = [&](int it) {
         i32x8 e;
-        asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(e) : "s"(p.blocks + 8 * (it / p.nh)) : "memory");
+        asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(e) : "s"(p.blocks + 8 * (item_base(it) / p.nh)) : "memory");
         return decode_from(e, it);
     };
     auto load_tiles = [&](const Item &s, int kb, uint16_t *Ks, uint16_t *Vs) {
@@ -291,7 +304,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     for (int k = 0;; k++) {
         // trace row of this item (100 MHz wall clock): start, end, HW_ID, XCC_ID, prologue end,
         // key loop end, workgroup, ordinal within the workgroup
-        uint64_t *const tr = (p.trace && tid == 0) ? p.trace + 8 * (size_t)item : nullptr;
+        uint64_t *const tr = (p.trace && tid == 0 && (item >> kItemBits) != 2) ? p.trace + 8 * (size_t)item_base(item) : nullptr;
         if (tr) {
             tr[0] = wall_clock64();
             tr[2] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
@@ -435,7 +448,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         // tile has landed. The next item's block entry loads during this wait.
         if (nxt >= 0)
             asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier"
-                         : "=s"(ne) : "s"(p.blocks + 8 * (nxt / p.nh)) : "memory");
+                         : "=s"(ne) : "s"(p.blocks + 8 * (item_base(nxt) / p.nh)) : "memory");
         else
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (tr) tr[4] = wall_clock64();

@@ -117,7 +117,8 @@ typedef struct {
                                  CLEF_HIP_OUT_F16. Non-finite V elements (V is bf16 here) are
                                  saturated to +-65504 and flag too */
     int32_t *ovf;             /* [T] int32 flags, set at the record's first pass row; may be NULL */
-    uint64_t *trace;          /* NULL, or [n_blk * nh][8] u64 per work item (query block, q head):
+    uint64_t *trace;          /* NULL, or [n_blk * nh][8] u64 per work item (query block, q head;
+                                 of a block split in halves by the schedule, the first half):
                                  start, end (100 MHz device wall clock), HW_ID and XCC_ID
                                  registers, end of the prologue, end of the key loop, workgroup,
                                  ordinal in the workgroup; the CLEF_PROFILE analogue
@@ -153,8 +154,12 @@ typedef struct {
  * (cost: the block's 64-key tiles plus a fixed per-item cost), within the workgroups of the XCD
  * that owns the item's q head when the heads divide evenly over the 8 XCDs (workgroup b runs on
  * XCD b % 8). blocks: the plan's host block list. Output: a header {0x53434844, n_blk, nh,
- * n_wg}, then n_wg + 1 item offsets per workgroup, then the items as block * nh + head, each
- * workgroup's longest first; clef_hip_attn_sched_size gives the entry count. */
+ * n_wg}, then n_wg + 1 item offsets per workgroup, then the items, each workgroup's longest
+ * first. An item is block * nh + head in bits 0-27 and, in bits 28-29, the block's rows it
+ * covers: 0 all of them; when the pass has fewer items than workgroups, a block of more than 64
+ * rows becomes two items, 1 (rows 0-63) and 2 (rows 64-127), so that more workgroups have work.
+ * Outputs are bitwise the same either way. clef_hip_attn_sched_size gives the room to allocate
+ * (an upper bound: the last offset is the item count). */
 int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg);
 
 bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,

@@ -257,6 +257,8 @@ def test_vision_mixed_images_and_f16():
     (24, 4, [1160, 890, 730, 425, 472, 136, 179, 104]),   # C1 shape: 864 items over the CUs
     (12, 4, [300, 77, 1030]),                              # heads not a multiple of 8: plain snake order
     (4, 1, [40, 3]),                                       # fewer items than CUs
+    (16, 4, [1024]),                                       # C0-like: every block split in halves
+    (8, 2, [700, 130, 64, 65, 1]),                         # halves only for blocks > 64 rows
 ])
 def test_persistent_grid_matches_one_item_per_workgroup(nh, nkv, lengths, monkeypatch):
     """The host schedule (clef_hip_attn_schedule over the CUs), the persistent grid's static

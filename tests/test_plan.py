@@ -99,27 +99,46 @@ def _sched(plan, nh, nkv, n_wg):
     return ok, out, err.value.decode()
 
 
+def _item_cost(plan, nh, it):
+    """An item's modelled cost: its 64-key tiles (a first half's keys end at its last row) + 3."""
+    e = plan.blocks_host[(it & ((1 << 28) - 1)) // nh]
+    k_len = min(int(e[4]), int(e[2]) + 64) if (it >> 28) == 1 else int(e[4])
+    return (k_len + 63) // 64 + 3
+
+
 @pytest.mark.parametrize("lengths,nh,nkv,n_wg", [
     ([1160, 890, 730, 425, 472, 136, 179, 104], 24, 4, 256),   # C1: heads split over the 8 XCDs
     ([16384], 24, 4, 256),
-    ([512] * 4, 16, 4, 256),
+    ([512] * 4, 16, 4, 256),                                     # as many items as workgroups
     ([300, 17, 1], 12, 4, 7),                                    # no XCD split
     ([5], 2, 1, 300),                                            # more workgroups than items
+    ([1000], 16, 4, 256),                                        # C0-like: blocks split in halves
+    ([700, 130, 64, 65, 1], 8, 2, 256),                          # halves only for blocks > 64 rows
 ])
 def test_schedule_covers_items_balanced(lengths, nh, nkv, n_wg):
-    """clef_hip_attn_schedule: every (block, head) item exactly once, each workgroup's items
-    longest first, items of an XCD's heads only on that XCD's workgroups, and greedy balance
-    (no workgroup above the mean load by more than one item's cost)."""
+    """clef_hip_attn_schedule: every (block, head) item exactly once, whole or (when the pass
+    has fewer items than workgroups and the block more than 64 rows) as its two 64-row halves;
+    each workgroup's items longest first, items of an XCD's heads only on that XCD's workgroups,
+    and greedy balance (no workgroup above the mean load by more than one item's cost)."""
     cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     plan = AttnPlan(cu, causal=True, device="cpu")
     ok, s, err = _sched(plan, nh, nkv, n_wg)
     assert ok, err
-    assert s[:4].tolist() == [0x53434844, plan.n_blk, nh, n_wg]   # the header the kernel checks
+    assert s[:4].tolist() == [0x53434844, plan.n_blk, nh, n_wg]   # the header names the plan
     s = s[4:]
-    off, items = s[: n_wg + 1], s[n_wg + 1:]
-    assert off[0] == 0 and (np.diff(off) >= 0).all() and off[-1] == plan.n_blk * nh
-    assert sorted(items.tolist()) == list(range(plan.n_blk * nh))
-    cost = lambda it: (int(plan.blocks_host[it // nh][4]) + 63) // 64 + 3
+    off = s[: n_wg + 1]
+    items = s[n_wg + 1: n_wg + 1 + off[-1]]
+    split_pass = plan.n_blk * nh < n_wg
+    want = []
+    for it in range(plan.n_blk * nh):
+        if split_pass and plan.blocks_host[it // nh][1] > 64:
+            want += [it | (1 << 28), it | (2 << 28)]
+        else:
+            want.append(it)
+    assert off[0] == 0 and (np.diff(off) >= 0).all() and off[-1] == len(want)
+    assert sorted(items.tolist()) == sorted(want)
+    cost = lambda it: _item_cost(plan, nh, it)
+    head = lambda it: (it & ((1 << 28) - 1)) % nh
     xh = nh // 8 if nh % 8 == 0 and ((nh // nkv) % (nh // 8) == 0 or (nh // 8) % (nh // nkv) == 0) else 0
     split = xh and n_wg % 8 == 0
     loads = []
@@ -128,14 +147,16 @@ def test_schedule_covers_items_balanced(lengths, nh, nkv, n_wg):
         c = [cost(it) for it in mine]
         assert c == sorted(c, reverse=True)
         if split:
-            assert all((it % nh) // xh == b % 8 for it in mine)
+            assert all(head(it) // xh == b % 8 for it in mine)
         loads.append(sum(c))
     groups = 8 if split else 1
     for x in range(groups):
         ld = loads[x::groups]
-        tot = sum(cost(it) for it in items.tolist() if not split or (it % nh) // xh == x)
-        biggest = max([cost(it) for it in items.tolist() if not split or (it % nh) // xh == x], default=0)
+        tot = sum(cost(it) for it in items.tolist() if not split or head(it) // xh == x)
+        biggest = max([cost(it) for it in items.tolist() if not split or head(it) // xh == x], default=0)
         assert max(ld) <= tot / len(ld) + biggest
+    if split_pass and len(want) <= n_wg and not split:
+        assert max(len(items[off[b]:off[b + 1]]) for b in range(n_wg)) == 1
 
 
 def test_schedule_errors():
@@ -154,6 +175,6 @@ def test_schedule_local_search_reaches_c1_bound():
     ok, s, err = _sched(plan, 24, 4, 256)
     assert ok, err
     off, items = s[4:261], s[261:]
-    cost = lambda it: (int(plan.blocks_host[it // 24][4]) + 63) // 64 + 3
+    cost = lambda it: _item_cost(plan, 24, it)
     loads = [sum(cost(it) for it in items[off[b]:off[b + 1]]) for b in range(256)]
     assert sum(loads) == 8784 and max(loads) <= 35
