@@ -224,8 +224,8 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         if (half == 1) {          // rows 0-63: a causal half sees keys up to its own last row
             s.nq = min(s.nq, 64);
             if (p.causal) s.k_len = min(s.k_len, s.q_pos0 + s.nq);
-        } else if (half == 2) {   // rows 64-127
-            s.q_row0 += 64; s.q_pos0 += 64; s.nq -= 64;
+        } else if (half == 2 && s.nq > 64) {   // rows 64-127 (of a smaller block: all of it, so
+            s.q_row0 += 64; s.q_pos0 += 64; s.nq -= 64;   // that no list reaches rows outside it)
         }
         s.flag_row = e[5];
         s.kh = s.h / (p.nh / p.nkv);

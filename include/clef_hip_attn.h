@@ -158,8 +158,9 @@ typedef struct {
  * first. An item is block * nh + head in bits 0-27 and, in bits 28-29, the block's rows it
  * covers: 0 all of them; when the pass has fewer items than workgroups, a block of more than 64
  * rows becomes two items, 1 (rows 0-63) and 2 (rows 64-127), so that more workgroups have work.
- * Outputs are bitwise the same either way. clef_hip_attn_sched_size gives the room to allocate
- * (an upper bound: the last offset is the item count). */
+ * Outputs are bitwise the same either way (the code 2 of a block of 64 rows or fewer runs the
+ * whole block, so no list reaches rows outside a block). clef_hip_attn_sched_size gives the room
+ * to allocate (an upper bound: the last offset is the item count). */
 int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg);
 
 bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,
