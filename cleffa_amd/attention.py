@@ -219,8 +219,9 @@ class TextAttention:
              schedule=True):
         """The C argument block. qkv rows in bf16 select the tensor-unit path, f32 rows the FP32
         path (qkv_type CLEF_HIP_QKV_F32, with f32 K and V planes). schedule: hand the bf16 core a
-        per-workgroup item split over the device's CUs (clef_hip_attn_schedule), else it falls
-        back to its static order; the FP32 core takes none."""
+        per-workgroup item split (clef_hip_attn_schedule) over the device's CUs (True) or over
+        that many workgroups (an int), else (False) it falls back to its static order; the FP32
+        core takes none."""
         T = plan.T
         dev = self.device
         fp32 = qkv.dtype == torch.float32
@@ -268,7 +269,10 @@ class TextAttention:
         a.trace = _ptr(trace)
         a.seq_start, a.qkv_type = _ptr(plan.seq_start), _lib.QKV_F32 if fp32 else _lib.QKV_BF16
         if schedule and plan.n_blk and not fp32:
-            n_wg = _device_cus(dev)
+            # True: one workgroup per CU; an int: that many workgroups
+            n_wg = _device_cus(dev) if schedule is True else int(schedule)
+            if n_wg <= 0:
+                raise ValueError(f"schedule: {n_wg} workgroups")
             a.sched, a.n_wg = _ptr(plan.schedule(self.nh, self.nkv, n_wg)), n_wg
         return a
 
