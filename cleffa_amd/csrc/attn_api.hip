@@ -253,12 +253,17 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
         // items of this XCD group, longest first (the plan's blocks already are)
         std::vector<std::pair<int, int>> its;   // (cost, item)
         for (int bi = 0; bi < n_blk; bi++) {
+            // a block of at most 64 rows runs k heads of a kv group at once (unless the pass
+            // splits blocks, which wants more items, not fewer)
+            const int pk = split ? 1 : clef_hip::pack_heads(blocks[8 * bi + 1], nh / nkv);
             for (int h = 0; h < nh; h++) {
                 if (groups != 1 && h / xh != x) continue;
                 const int it = bi * nh + h;
                 if (split && blocks[8 * bi + 1] > 64) {   // the block's rows 0-63 and 64-127
                     its.push_back({cost_of(it | (1 << 28)), it | (1 << 28)});
                     its.push_back({cost_of(it | (2 << 28)), it | (2 << 28)});
+                } else if (pk > 1) {                      // heads h .. h + pk - 1 (group-aligned)
+                    if (h % pk == 0) its.push_back({cost_of(it | (3 << 28)), it | (3 << 28)});
                 } else {
                     its.push_back({cost_of(it), it});
                 }

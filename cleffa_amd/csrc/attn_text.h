@@ -115,10 +115,21 @@ __device__ __forceinline__ int sload(const int32_t *ptr) {
 }
 // A schedule item: block * nh + head in bits 0-27, and in bits 28-29 the rows of the block it
 // covers: 0 all, 1 rows 0-63, 2 rows 64-127 (a pass with fewer items than workgroups splits its
-// blocks so that every workgroup has work). A row's arithmetic does not depend on the split:
-// each 16-row wave runs the key tiles up to its own last row, from the record's first key.
+// blocks so that every workgroup has work), or 3: the block's rows (at most 64) for heads
+// h .. h + k - 1 of one kv group, ceil(rows / 16) waves per head (pack_heads), which share its
+// key tiles. A row's arithmetic does not depend on any of this: each 16-row wave runs the key
+// tiles up to its own last row, from the record's first key.
 constexpr int kItemBits = 28;
 __device__ __forceinline__ int item_base(int it) { return it & ((1 << kItemBits) - 1); }
+// Heads per packed item of a block of nq <= 64 rows: the largest divisor of the kv group size
+// that fits 8 waves at ceil(nq / 16) waves per head (the host schedule uses the same rule).
+__host__ __device__ inline int pack_heads(int nq, int group) {
+    const int wph = (nq + 15) / 16;
+    if (nq <= 0 || nq > 64) return 1;
+    for (int k = 8 / wph; k > 1; k--)
+        if (group % k == 0) return k;
+    return 1;
+}
 struct ItemList {
     int n_items, per_x, gx, xh, nh, s0, s1;
     const int32_t *list;
@@ -143,7 +154,7 @@ struct ItemList {
         if (list) {
             if (s0 + k >= s1) return -1;
             const int it = sload(list + s0 + k);
-            return (it >= 0 && (it >> kItemBits) <= 2 && item_base(it) < n_items) ? it : -1;   // never an item outside the plan
+            return (it >= 0 && item_base(it) < n_items) ? it : -1;   // never an item outside the plan
         }
         if (xh && gx && ((int)gridDim.x & 7) == 0) {
             const int x = blockIdx.x & 7, wl = blockIdx.x >> 3;
@@ -211,6 +222,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     // Item state: the block entry and the lane's query row.
     struct Item {
         int q_row0, nq, q_pos0, k_row0, k_len, flag_row, h, kh, n_tiles;
+        int wph, hk;   // waves per head (8: one head on all waves), heads in the item
         const uint16_t *kbase, *vbase;
     };
     // The block entry is read with a scalar load: the compiler would read it with vector loads
@@ -227,8 +239,14 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         } else if (half == 2 && s.nq > 64) {   // rows 64-127 (of a smaller block: all of it, so
             s.q_row0 += 64; s.q_pos0 += 64; s.nq -= 64;   // that no list reaches rows outside it)
         }
+        const int group = p.nh / p.nkv;
+        s.wph = 8; s.hk = 1;
+        if (half == 3) {   // heads h .. h + k - 1, all in h's kv group (else the item runs head h)
+            const int k = pack_heads(s.nq, group);
+            if (k > 1 && s.h % group + k <= group) { s.wph = (s.nq + 15) / 16; s.hk = k; }
+        }
         s.flag_row = e[5];
-        s.kh = s.h / (p.nh / p.nkv);
+        s.kh = s.h / group;
         s.n_tiles = (s.k_len + BK - 1) / BK;
         s.kbase = p.k_plane + ((size_t)s.kh * p.kvT + s.k_row0) * HD;
         s.vbase = p.vt_plane + (size_t)s.kh * HD * p.kvT + s.k_row0;
@@ -259,14 +277,17 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         // item and tile loops, its 16 per-lane offsets would stay live and spill.
         int ln = lane;
         asm volatile("" : "+v"(ln));
+        // wave w loads LDS rows 16w .. 16w + 15, the rows it runs: head slot w / wph, block rows
+        // 16 (w mod wph) + [0, 16)
+        const int jw = wave_s / s.wph, hw = s.h + min(jw, s.hk - 1), r0w = (wave_s - jw * s.wph) * ROWS;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int grp = wave_s * 8 + j;   // 64-slot group, 0..63
             const int row = grp * 2 + (ln >> 5);
             const int c = (ln & 31) ^ (row & 15);
-            int rc = min(row, s.nq - 1);
+            int rc = min(r0w + (row & 15), s.nq - 1);
             uint16_t *dst = (grp < 32 ? G0 : G1) + (grp & 31) * 512;
-            __builtin_amdgcn_global_load_lds((const void *)(p.qkv + ((size_t)s.q_row0 + rc) * p.row + (size_t)s.h * 2 * HD + off + c * 8),
+            __builtin_amdgcn_global_load_lds((const void *)(p.qkv + ((size_t)s.q_row0 + rc) * p.row + (size_t)hw * 2 * HD + off + c * 8),
                                              (lds_void *)dst, 16, 0, 0);
         }
     };
@@ -274,7 +295,8 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     float4 csv[R > 0 ? R : 1][4];
     auto load_cs = [&](const Item &s) {
         if (NROT > 0 && p.rope_cs) {
-            const int my_q = wave * ROWS + q16;
+            const int jw = wave_s / s.wph;
+            const int my_q = (wave_s - jw * s.wph) * ROWS + q16;
             const size_t qrow = (size_t)s.q_row0 + (my_q < s.nq ? my_q : 0);
             const float *cs = p.rope_cs + qrow * (NROT / 2) * 2;
 #pragma unroll
@@ -312,11 +334,13 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             tr[6] = blockIdx.x;
             tr[7] = k;
         }
-        const int my_q = wave * ROWS + q16;
-        const bool q_valid = my_q < cur.nq;
+        // this wave's head and rows in the item (one head on all waves but in a packed item)
+        const int jw = wave_s / cur.wph, row0w = (wave_s - jw * cur.wph) * ROWS, my_h = cur.h + jw;
+        const int my_q = row0w + q16;
+        const bool q_valid = jw < cur.hk && my_q < cur.nq;
         const int qpos = cur.q_pos0 + my_q;
-        const bool wave_live = wave * ROWS < cur.nq;
-        const int wave_last_pos = cur.q_pos0 + wave * ROWS + ROWS - 1;
+        const bool wave_live = jw < cur.hk && row0w < cur.nq;
+        const int wave_last_pos = cur.q_pos0 + row0w + ROWS - 1;
         const int k_len = cur.k_len, n_tiles = cur.n_tiles;
 
         // ---- Q prologue: lane holds Q[my_q][c*32 + 8g + j], the B operand of chunk c.
@@ -512,7 +536,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                 static_for<DEPTH>([&](auto I) { vring[decltype(I)::value] = vread(I); });
                 // Online softmax in the exp2 domain. Masked scores are -inf, so their P is an exact
                 // zero and a tile past a row's diagonal rescales the row by exactly 1.
-                if ((kb + BK > k_len) || (p.causal && kb + BK - 1 > cur.q_pos0 + wave * ROWS)) {
+                if ((kb + BK > k_len) || (p.causal && kb + BK - 1 > cur.q_pos0 + row0w)) {
                     // element (kt, i) is key kb + 32(kt>>1) + 8g + 4(kt&1) + i
                     const int lim = min(k_len - 1, p.causal ? qpos : k_len - 1) - kb - 8 * g;
 #pragma unroll
@@ -594,7 +618,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         const float l_row = xrow_sum(l_run);   // outside the row-divergent branch: lanes exchange values
         const int last_buf = (par + n_tiles + 1) & 1;
         const int gate_buf = last_buf ^ 1;
-        const int q_row0 = cur.q_row0, flag_row = cur.flag_row, h = cur.h;
+        const int q_row0 = cur.q_row0, flag_row = cur.flag_row, h = my_h;
         item = nxt;
         if (item >= 0) {
             cur = decode_from(ne, item);

@@ -155,12 +155,15 @@ typedef struct {
  * that owns the item's q head when the heads divide evenly over the 8 XCDs (workgroup b runs on
  * XCD b % 8). blocks: the plan's host block list. Output: a header {0x53434844, n_blk, nh,
  * n_wg}, then n_wg + 1 item offsets per workgroup, then the items, each workgroup's longest
- * first. An item is block * nh + head in bits 0-27 and, in bits 28-29, the block's rows it
- * covers: 0 all of them; when the pass has fewer items than workgroups, a block of more than 64
- * rows becomes two items, 1 (rows 0-63) and 2 (rows 64-127), so that more workgroups have work.
- * Outputs are bitwise the same either way (the code 2 of a block of 64 rows or fewer runs the
- * whole block, so no list reaches rows outside a block). clef_hip_attn_sched_size gives the room
- * to allocate (an upper bound: the last offset is the item count). */
+ * first. An item is block * nh + head in bits 0-27 and, in bits 28-29, what it runs: 0 the whole
+ * block for that head; when the pass has fewer items than workgroups, a block of more than 64
+ * rows becomes two items, 1 (rows 0-63) and 2 (rows 64-127), so that more workgroups have work;
+ * otherwise a block of at most 64 rows runs k heads h .. h + k - 1 of one kv group in one item,
+ * 3 (k the largest divisor of nh / nkv with k * ceil(rows / 16) <= 8), so that they share its key
+ * tiles. Outputs are bitwise the same in every case (a code 2 of a block of 64 rows or fewer runs
+ * the whole block, a code 3 that does not fit its kv group runs head h only, so no list reaches
+ * rows or heads outside its item). clef_hip_attn_sched_size gives the room to allocate (an upper
+ * bound: the last offset is the item count). */
 int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg);
 
 bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,
