@@ -237,9 +237,11 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
     const long need = 4L + n_wg + 1 + (long)n_blk * nh * (split ? 2 : 1);
     if (need > max_sched) return fail(err, errlen, "schedule needs %ld entries, room for %d", need, max_sched);
     // cost of an item in 64-key tiles: its tiles plus the prologue / epilogue (Q rows, gate,
-    // output stores), measured at about three tiles' time per item. A first half's keys end at
-    // its last row when the pass is causal (the estimate assumes it is).
-    constexpr int kFixed = 3;
+    // output stores). Measured at about three tiles' time per item, but a weight of 6 balances
+    // C1 best (core 74-76.5 us against 76-78 us at 3, in two calls; 8 and 10 lose again): it
+    // spreads the item counts, and the items' real durations vary more than their tiles do. A
+    // first half's keys end at its last row when the pass is causal (the estimate assumes it is).
+    constexpr int kFixed = 6;
     const int xh = (nh % 8 == 0 && ((nh / nkv) % (nh / 8) == 0 || (nh / 8) % (nh / nkv) == 0)) ? nh / 8 : 0;
     const int groups = (xh && n_wg % 8 == 0) ? 8 : 1;
     auto cost_of = [&](int item) {
