@@ -54,7 +54,7 @@ def test_random_text_pass(seed):
     assert_close(sched.float().cpu().numpy(), oracle_text(w), what=f"seed {seed}")
 
 
-@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("seed", range(10))
 def test_random_prefix_pass_equals_full_pass(seed):
     """Records whose first rows are already in the planes (a prefix pass: each record's last
     tokens as queries, all its tokens as keys) give bitwise the rows of the full pass that wrote
@@ -65,7 +65,8 @@ def test_random_prefix_pass_equals_full_pass(seed):
     # key offsets must be multiples of 8: every record but the last is a multiple of 8 long
     full = [8 * int(rng.integers(2, 50)) for _ in range(n - 1)] + [int(rng.integers(9, 400))]
     new = [int(rng.integers(1, f)) for f in full]
-    _say(f"[sweep] prefix seed {seed}: full {full} new {new} heads {nh}/{nkv}")
+    n_wg = int(rng.choice([8, 37, 256]))   # few workgroups: small blocks packed; many: split
+    _say(f"[sweep] prefix seed {seed}: full {full} new {new} heads {nh}/{nkv} n_wg {n_wg}")
     w = workloads.text_inputs(full, nh, nkv, seed=seed)
     att = TextAttention(nh, nkv, 256, 64, rope_theta=1e7)
     ck = np.concatenate([[0], np.cumsum(full)]).astype(np.int32)
@@ -77,7 +78,7 @@ def test_random_prefix_pass_equals_full_pass(seed):
     ref = att.forward(qkv, qn, kn, p3, plan_full, k_plane=kp, vt_plane=vt, kvT=kvT)
     pick = torch.from_numpy(np.concatenate([np.arange(ck[r + 1] - new[r], ck[r + 1]) for r in range(n)])).cuda()
     part = att.forward(qkv[pick].contiguous(), qn, kn, p3[pick].contiguous(), plan_new, k_plane=kp, vt_plane=vt,
-                       kvT=kvT)
+                       kvT=kvT, schedule=n_wg)
     torch.cuda.synchronize()
     assert torch.equal(part.view(torch.int16), ref[pick].view(torch.int16))
 
