@@ -48,12 +48,13 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="C1", choices=["C0", "C1", "C2", "C3", "C4", "P", "O", "G", "M"],
-                    help="C0-C4: attention configurations; P: prefix-cache growth copy (HBM-bound); "
+    ap.add_argument("--config", default="C1", choices=["C0", "C1", "C2", "C3", "C4", "S", "P", "O", "G", "M"],
+                    help="C0-C4: attention configurations; S: 256 records x 16 tokens (short prompts); "
+                         "P: prefix-cache growth copy (HBM-bound); "
                          "O: Omni attention (hd 128, FP32, 16,344 tokens); G: the QKV and o_proj GEMMs around C1")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--fp32", action="store_true",
-                    help="C0-C3 in the FP32 mode (f32 qkv rows, FP32 planes and products: the reference's "
+                    help="C0-C3 and S in the FP32 mode (f32 qkv rows, FP32 planes and products: the reference's "
                          "FP32 kernels); the roofline is then priced against the fp32 MFMA peak")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
@@ -71,7 +72,7 @@ def build_step(cfg, seed, fp32=False):
     w = workloads.config(cfg, seed=seed, device=dev)
     if fp32:
         if cfg == "C4":
-            raise SystemExit("--fp32 applies to the text configurations C0-C3")
+            raise SystemExit("--fp32 applies to the text configurations C0-C3 and S")
         w["qkv"] = w["qkv"].float()
     if cfg == "C4":
         vis = VisionAttention(w["heads"], w["hd"], device=dev)
@@ -113,7 +114,9 @@ def build_step(cfg, seed, fp32=False):
              "C1": "C1 packed varlen causal micro-batch: 8 records, 4,096 tokens, 24/4 heads, hd 256, "
                    "fused q/k RMSNorm + rotary(64, theta 1e7) + sigmoid gate",
              "C2": "C2 single causal request: 16,384 tokens, 24/4 heads, hd 256, fused prologue/gate",
-             "C3": "C3 prefix-cache continuation: 4 x (2,048 cached + 512 new), 16/4 heads, hd 256"}
+             "C3": "C3 prefix-cache continuation: 4 x (2,048 cached + 512 new), 16/4 heads, hd 256",
+             "S": "S batch of short records: 256 x 16 tokens (4,096 tokens), 24/4 heads, hd 256, fused "
+                  "q/k RMSNorm + rotary(64, theta 1e7) + sigmoid gate"}
     # the attention kernel alone: Q and gate rows read once, each K / V plane row read once, O
     # written once (the scope of roofline.traffic)
     kv_rows = int(w["cu_seqlens_k"][-1]) if cfg == "C3" else T

@@ -249,29 +249,46 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
         const int k_len = (item >> 28) == 1 ? std::min(e[4], e[2] + 64) : e[4];
         return (k_len + 63) / 64 + kFixed;
     };
+    // Every item with its cost; then each to an XCD group: its head's, or for a packed item whose
+    // heads span several groups (all of them hold the kv head's planes), the least loaded of
+    // them, taking the items longest first. Without that, a pass of short records, all packed,
+    // would leave the groups of the heads that never start a packed item idle.
+    std::vector<std::pair<int, int>> all;   // (cost, item)
+    for (int bi = 0; bi < n_blk; bi++) {
+        // a block of at most 64 rows runs k heads of a kv group at once (unless the pass splits
+        // blocks, which wants more items, not fewer)
+        const int pk = split ? 1 : clef_hip::pack_heads(blocks[8 * bi + 1], nh / nkv);
+        for (int h = 0; h < nh; h++) {
+            const int it = bi * nh + h;
+            if (split && blocks[8 * bi + 1] > 64) {   // the block's rows 0-63 and 64-127
+                all.push_back({cost_of(it | (1 << 28)), it | (1 << 28)});
+                all.push_back({cost_of(it | (2 << 28)), it | (2 << 28)});
+            } else if (pk > 1) {                      // heads h .. h + pk - 1 (group-aligned)
+                if (h % pk == 0) all.push_back({cost_of(it | (3 << 28)), it | (3 << 28)});
+            } else {
+                all.push_back({cost_of(it), it});
+            }
+        }
+    }
+    std::stable_sort(all.begin(), all.end(), [](const std::pair<int, int> &u, const std::pair<int, int> &v) { return u.first > v.first; });
+    std::vector<std::vector<std::pair<int, int>>> per_x(groups);
+    std::vector<long> xload(groups, 0);
+    for (const auto &c : all) {
+        int x = 0;
+        if (groups != 1) {
+            const int base = c.second & ((1 << 28) - 1), h0 = base % nh;
+            const int hk = (c.second >> 28) == 3 ? clef_hip::pack_heads(blocks[8 * (base / nh) + 1], nh / nkv) : 1;
+            x = h0 / xh;
+            for (int y = h0 / xh + 1; y <= (h0 + hk - 1) / xh; y++)
+                if (xload[y] < xload[x]) x = y;
+        }
+        per_x[x].push_back(c);
+        xload[x] += c.first;
+    }
     std::vector<std::vector<int>> lists(n_wg);
     std::vector<long> load(n_wg, 0);
     for (int x = 0; x < groups; x++) {
-        // items of this XCD group, longest first (the plan's blocks already are)
-        std::vector<std::pair<int, int>> its;   // (cost, item)
-        for (int bi = 0; bi < n_blk; bi++) {
-            // a block of at most 64 rows runs k heads of a kv group at once (unless the pass
-            // splits blocks, which wants more items, not fewer)
-            const int pk = split ? 1 : clef_hip::pack_heads(blocks[8 * bi + 1], nh / nkv);
-            for (int h = 0; h < nh; h++) {
-                if (groups != 1 && h / xh != x) continue;
-                const int it = bi * nh + h;
-                if (split && blocks[8 * bi + 1] > 64) {   // the block's rows 0-63 and 64-127
-                    its.push_back({cost_of(it | (1 << 28)), it | (1 << 28)});
-                    its.push_back({cost_of(it | (2 << 28)), it | (2 << 28)});
-                } else if (pk > 1) {                      // heads h .. h + pk - 1 (group-aligned)
-                    if (h % pk == 0) its.push_back({cost_of(it | (3 << 28)), it | (3 << 28)});
-                } else {
-                    its.push_back({cost_of(it), it});
-                }
-            }
-        }
-        std::stable_sort(its.begin(), its.end(), [](const std::pair<int, int> &u, const std::pair<int, int> &v) { return u.first > v.first; });
+        const std::vector<std::pair<int, int>> &its = per_x[x];   // longest first
         for (const auto &it : its) {
             int best = -1;
             for (int b = x; b < n_wg; b += groups)

@@ -9,6 +9,8 @@ C2  one causal request of 16,384 tokens, 24/4, same prologue/epilogue as C1.
 C3  prefix-cache continuation: 4 records x (2,048 cached K/V rows + 512 new queries at
     positions 2,048..2,559), 16/4 heads, hd 256.
 C4  vision: 4 images x 1,024 patches (32x32 grid), bidirectional, 16 heads, hd 72, 2-D rotary.
+S   a batch of short records: 256 records x 16 tokens (4,096 tokens), 24/4 heads, hd 256, C1's
+    prologue and gate (not a BASELINE configuration: the serving case of many short prompts).
 
 Record lengths come from a numpy PCG64 stream so they are identical on every machine; the
 tensor values come from a torch generator on the target device.
@@ -88,6 +90,10 @@ def config(name, seed=0, device="cpu"):
         return w
     if name == "C2":
         w = text_inputs([16384], 24, 4, seed=seed, device=device, outlier_frac=0)
+        w.update(gate=True, theta=1e7)
+        return w
+    if name == "S":
+        w = text_inputs([16] * 256, 24, 4, seed=seed, device=device)
         w.update(gate=True, theta=1e7)
         return w
     if name == "C3":

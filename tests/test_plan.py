@@ -114,6 +114,7 @@ def _item_cost(plan, nh, it):
     ([5], 2, 1, 300),                                            # more workgroups than items
     ([1000], 16, 4, 256),                                        # C0-like: blocks split in halves
     ([700, 130, 64, 65, 1], 8, 2, 256),                          # halves only for blocks > 64 rows
+    ([16] * 256, 24, 4, 256),                                    # short records: every block packed
 ])
 def test_schedule_covers_items_balanced(lengths, nh, nkv, n_wg):
     """clef_hip_attn_schedule: every (block, head) item exactly once, whole or (when the pass
@@ -167,17 +168,22 @@ def test_schedule_covers_items_balanced(lengths, nh, nkv, n_wg):
         mine = items[off[b]:off[b + 1]].tolist()
         c = [cost(it) for it in mine]
         assert c == sorted(c, reverse=True)
-        if split:
-            assert all(head(it) // xh == b % 8 for it in mine)
+        if split:   # on an XCD of one of its heads (a packed item may span two)
+            for it in mine:
+                hk = pack(int(plan.blocks_host[(it & ((1 << 28) - 1)) // nh][1])) if it >> 28 == 3 else 1
+                assert head(it) // xh <= b % 8 <= (head(it) + hk - 1) // xh
         loads.append(sum(c))
     groups = 8 if split else 1
     for x in range(groups):
         ld = loads[x::groups]
-        tot = sum(cost(it) for it in items.tolist() if not split or head(it) // xh == x)
-        biggest = max([cost(it) for it in items.tolist() if not split or head(it) // xh == x], default=0)
+        mine = [it for b in range(x, n_wg, groups) for it in items[off[b]:off[b + 1]].tolist()]
+        tot = sum(cost(it) for it in mine)
+        biggest = max([cost(it) for it in mine], default=0)
         assert max(ld) <= tot / len(ld) + biggest
     if split_pass and len(want) <= n_wg and not split:
         assert max(len(items[off[b]:off[b + 1]]) for b in range(n_wg)) == 1
+    if len(want) >= n_wg:   # every workgroup has work, also when every item is packed
+        assert min(len(items[off[b]:off[b + 1]]) for b in range(n_wg)) >= 1
 
 
 def test_schedule_errors():
