@@ -14,7 +14,7 @@ OUT_BF16, OUT_F16, OUT_F32 = 0, 1, 2
 QKV_BF16, QKV_F32 = 0, 1
 VIS_SCRATCH_BYTES = 64 << 20
 BLOCK_Q = 128
-KV_ALIGN = 64
+KV_ALIGN = 8
 BLOCK_INTS = 8
 
 # Every symbol include/clef_hip_attn.h declares.

@@ -120,7 +120,8 @@ class AttnPlan:
         max_blk = lib.clef_hip_attn_plan_max_blocks(self.n_seq, self.T)
         blocks = np.zeros((max(max_blk, 1), BLOCK_INTS), dtype=np.int32)
         tok_kv = np.zeros(max(self.T, 1), dtype=np.int32)
-        # plane rows: a fresh pass pads each record to 64 rows; a prefix pass ends at cu_k[-1] + 64
+        # plane rows: a fresh pass starts each record at a multiple of 8 rows and reads whole 64-key
+        # tiles from it; a prefix pass ends at cu_k[-1] + 64 (a bound: the plan reports kv_rows)
         max_kv = (self.T + 64 * self.n_seq if self.cu_k is None else int(self.cu_k[-1]) + 64) + 64
         kv_tok = np.zeros(max_kv, dtype=np.int32)
         n_blk, kv_rows = ctypes.c_int(0), ctypes.c_int(0)

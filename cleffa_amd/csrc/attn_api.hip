@@ -390,14 +390,17 @@ bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int
             ents.push_back(e);
         }
     }
-    // rows per head the planes need: the fills read whole 64-key tiles from each record's first key
+    // rows per head the planes need: the fills read whole 64-key tiles from each record's first
+    // key (past a record's last key they read the next record's rows, masked in the scores and
+    // zeroed in the V tile, or the slack at the end)
+    constexpr int kTileKeys = 64;
     int total_kv = 0;
     kv_off = 0;
     for (int r = 0; r < n_seq; r++) {
         const int nq = cu_q[r + 1] - cu_q[r];
         const int nk = cu_k ? cu_k[r + 1] - cu_k[r] : nq;
         const int k0 = cu_k ? cu_k[r] : kv_off;
-        total_kv = std::max(total_kv, k0 + (nk + CLEF_HIP_KV_ALIGN - 1) / CLEF_HIP_KV_ALIGN * CLEF_HIP_KV_ALIGN);
+        total_kv = std::max(total_kv, k0 + (nk + kTileKeys - 1) / kTileKeys * kTileKeys);
         if (!cu_k) kv_off += (nq + CLEF_HIP_KV_ALIGN - 1) / CLEF_HIP_KV_ALIGN * CLEF_HIP_KV_ALIGN;
     }
     if ((int)ents.size() > max_blocks) return fail(err, errlen, "plan needs %zu blocks, room for %d", ents.size(), max_blocks);

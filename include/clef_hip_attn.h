@@ -42,7 +42,7 @@ extern "C" {
 #define CLEF_HIP_OUT_F32 2  /* f32, unrounded: a store width only; FP32 arithmetic is qkv_type CLEF_HIP_QKV_F32 */
 
 #define CLEF_HIP_BLOCK_Q 128  /* query rows per block */
-#define CLEF_HIP_KV_ALIGN 64  /* kv row alignment of each record in a fresh pass */
+#define CLEF_HIP_KV_ALIGN 8   /* kv row alignment of each record in a fresh pass (V^T runs of 8 keys) */
 #define CLEF_HIP_BLOCK_INTS 8 /* int32 per block entry */
 
 /* Library version and the wave size the kernels were compiled for (64). The Metal backend
@@ -62,7 +62,8 @@ int clef_hip_attn_plan_max_blocks(int n_seq, int Tq);
 /* Host-only: builds the query-block list and the kv-row map of a pass (clef_metal.m:1243-1257
  * block list; clef.c:470-497 packing). cu_q[n_seq+1] are the records' pass-row bounds
  * (seq_bounds). cu_k = NULL is a fresh pass: every record's keys are its own queries and the
- * plan lays them out at 64-aligned kv rows. cu_k != NULL is a prefix-cache pass
+ * plan lays them out at kv rows aligned to CLEF_HIP_KV_ALIGN (8), with *kv_rows covering a whole
+ * 64-key tile from each record's first key. cu_k != NULL is a prefix-cache pass
  * (clef_gpu_forward_prefix, clef_metal.m:1640-1666): record r's keys occupy kv rows
  * cu_k[r] .. cu_k[r+1] (multiples of 8), its first cu_k[r+1]-cu_k[r]-(cu_q[r+1]-cu_q[r]) keys are
  * cached, and its queries are the last tokens. causal = 0 gives bidirectional attention within

@@ -25,7 +25,7 @@ def _check_plan(cu_q, cu_k, causal):
         if cu_k is not None:
             assert k_row0 == cu_k[rec]
         # whole 64-key tiles from the record's first key stay inside the planes
-        assert k_row0 + -(-lk // KV_ALIGN) * KV_ALIGN <= plan.kv_rows
+        assert k_row0 + -(-lk // 64) * 64 <= plan.kv_rows
     assert (seen == 1).all(), "every pass row in exactly one block"
     assert (np.diff(b[:, 4]) <= 0).all(), "blocks ordered longest first"
     # pass row -> kv row: a record's tokens are its last keys, in order
