@@ -378,10 +378,11 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                 const float inv = rsqrtf(ss / (float)HD + p.eps);
 #pragma unroll
                 for (int c = 0; c < NC; c++) {
-                    bf16x8 r0 = lds_read16<0>(qn_addr + 4u * (c * 32 + 8 * gg));
-                    bf16x8 r1 = lds_read16<16>(qn_addr + 4u * (c * 32 + 8 * gg));
-                    lds_wait<0>(r0);
-                    lds_wait<0>(r1);
+                    // both reads and their wait in one statement: nothing can touch the
+                    // registers while the reads are in flight
+                    bf16x8 r0, r1;
+                    asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
+                                 : "=&v"(r0), "=&v"(r1) : "v"(qn_addr + 4u * (c * 32 + 8 * gg)) : "memory");
                     const float4 w0 = __builtin_bit_cast(float4, r0), w1 = __builtin_bit_cast(float4, r1);
                     const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
@@ -630,18 +631,16 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             const float il = l_row > 0.f ? 1.f / l_row : 0.f;
             const size_t t = (size_t)q_row0 + my_q;
             int32_t *flag = p.ovf ? p.ovf + flag_row : nullptr;
-            // gate reads as asm: the compiler would wait for the in-flight fills before them
+            // Gate chunks come two at a time, both reads and their wait in one statement, so
+            // nothing can copy their registers while the reads are in flight (split into a read
+            // and a later wait, the compiler moved ring registers between the two), and the wait
+            // is for LDS alone, not for the next item's loads in flight.
             int ln = lane;
             asm volatile("" : "+v"(ln));
             const int mq = wave_s * ROWS + (ln & 15), gg = ln >> 4;
             const unsigned gbase = lds_addr(gate_buf ? k1s : k0s) + (mq < 64 ? 0u : 2u * 2 * KTILE) + (unsigned)(mq & 63) * 512u;
-            // gate chunks read two ahead of their use (a ring of 3), the last waits draining it
-            bf16x8 gring[3];
-            auto gread = [&](int u) { return lds_read16<0>(gbase + (unsigned)(((4 * u + gg) ^ (mq & 15)) * 16)); };
-            if (p.gate) {
-                gring[0] = gread(0);
-                gring[1] = gread(1);
-            }
+            auto gaddr = [&](int u) { return gbase + (unsigned)(((4 * u + gg) ^ (mq & 15)) * 16); };
+            u32x4 gq[2];
             static_for<8>([&](auto U) {
                 constexpr int u = decltype(U)::value;
                 const int d0 = 32 * u + 8 * g;
@@ -652,10 +651,10 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                     v[4 + i] = o[2 * u + 1][i] * il;
                 }
                 if (p.gate) {
-                    if constexpr (u + 2 < 8) gring[(u + 2) % 3] = gread(u + 2);
-                    bf16x8 gr = gring[u % 3];
-                    lds_wait<(u + 2 < 8) ? 2 : (u + 1 < 8 ? 1 : 0)>(gr);
-                    const u32x4 gw = __builtin_bit_cast(u32x4, gr);
+                    if constexpr ((u & 1) == 0)
+                        asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                                     : "=&v"(gq[0]), "=&v"(gq[1]) : "v"(gaddr(u)), "v"(gaddr(u + 1)) : "memory");
+                    const u32x4 gw = gq[u & 1];
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         v[2 * j] *= sigmoidf(bf_lo(gw[j]));
