@@ -84,6 +84,16 @@ template <int N>
 __device__ __forceinline__ void lds_wait(bf16x8 &r) {
     asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
 }
+// One wait for two reads (the two operands of a pair of products): half the waits, and the
+// compiler's wait state after the asm falls before the first product only.
+template <int N>
+__device__ __forceinline__ void lds_wait2(bf16x8 &r0, bf16x8 &r1) {
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(r0), "+v"(r1) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void lds_wait4(bf16x8 &r0, bf16x8 &r1, bf16x8 &r2, bf16x8 &r3) {
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3) : "i"(N));
+}
 __device__ __forceinline__ unsigned lds_addr(const uint16_t *p) {
     return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) uint16_t *)p;
 }
@@ -508,24 +518,30 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                 // S^T: 32 MFMAs (4 key tiles x 8 dim chunks), chunk-major so consecutive products
                 // go to different accumulators. K operands are read DEPTH steps ahead of their
                 // product so the LDS latency overlaps the matrix work.
-                constexpr int DEPTH = 6, QK = 4 * NC;
+                constexpr int DEPTH = 8, QK = 4 * NC;
                 f32x4 s[4];
                 bf16x8 ring[DEPTH];
                 static_for<DEPTH>([&](auto I) {
                     constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
                     ring[st] = lds_read16<buf * 2 * KTILE + (c >> 2) * 256>(ka[kt][c & 3]);
                 });
-                static_for<QK>([&](auto I) {
-                    constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
-                    constexpr int ahead = (QK - 1 - st) < (DEPTH - 1) ? (QK - 1 - st) : (DEPTH - 1);
-                    bf16x8 a = ring[st % DEPTH];
-                    lds_wait<ahead>(a);
-                    if constexpr (c == 0) s[kt] = f32x4{-msub, -msub, -msub, -msub};
-                    s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), qf[c], s[kt], 0, 0, 0);
-                    if constexpr (st + DEPTH < QK) {
-                        constexpr int n = st + DEPTH, nkt = n & 3, nc = n >> 2;
-                        ring[st % DEPTH] = lds_read16<buf * 2 * KTILE + (nc >> 2) * 256>(ka[nkt][nc & 3]);
-                    }
+                // steps in pairs: one wait covers both operands (reads are issued up to step
+                // 2p + DEPTH - 1 when pair p's wait runs)
+                static_for<QK / 4>([&](auto P) {
+                    constexpr int st = 4 * decltype(P)::value;
+                    constexpr int last = (st + DEPTH - 1) < (QK - 1) ? (st + DEPTH - 1) : (QK - 1);
+                    bf16x8 a[4] = {ring[st % DEPTH], ring[(st + 1) % DEPTH], ring[(st + 2) % DEPTH], ring[(st + 3) % DEPTH]};
+                    lds_wait4<last - (st + 3)>(a[0], a[1], a[2], a[3]);
+                    static_for<4>([&](auto H) {
+                        constexpr int sp = st + decltype(H)::value, kt = sp & 3, c = sp >> 2;
+                        if constexpr (c == 0) s[kt] = f32x4{-msub, -msub, -msub, -msub};
+                        s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a[decltype(H)::value]), qf[c], s[kt], 0, 0, 0);
+                    });
+                    static_for<4>([&](auto H) {
+                        constexpr int n = st + decltype(H)::value + DEPTH, nkt = n & 3, nc = n >> 2;
+                        if constexpr (n < QK)
+                            ring[(st + decltype(H)::value) % DEPTH] = lds_read16<buf * 2 * KTILE + (nc >> 2) * 256>(ka[nkt][nc & 3]);
+                    });
                 });
                 // first V operands, in flight during the softmax
                 auto vread = [&](auto I) {   // step st = 16 * kc + mt
@@ -586,13 +602,19 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
 #pragma unroll
                     for (int mt = 0; mt < 16; mt++) o[mt] *= alpha;
                 }
-                static_for<32>([&](auto I) {   // O^T: 32 MFMAs over 16 rotating accumulators, same read-ahead
-                    constexpr int st = decltype(I)::value, mt = st & 15, kc = st >> 4;
-                    constexpr int ahead = (31 - st) < (DEPTH - 1) ? (31 - st) : (DEPTH - 1);
-                    bf16x8 a = vring[st % DEPTH];
-                    lds_wait<ahead>(a);
-                    o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[kc], o[mt], 0, 0, 0);
-                    if constexpr (st + DEPTH < 32) vring[st % DEPTH] = vread(std::integral_constant<int, st + DEPTH>{});
+                static_for<8>([&](auto P) {   // O^T: 32 MFMAs over 16 rotating accumulators, same read-ahead, in fours
+                    constexpr int st = 4 * decltype(P)::value;
+                    constexpr int last = (st + DEPTH - 1) < 31 ? (st + DEPTH - 1) : 31;
+                    bf16x8 a[4] = {vring[st % DEPTH], vring[(st + 1) % DEPTH], vring[(st + 2) % DEPTH], vring[(st + 3) % DEPTH]};
+                    lds_wait4<last - (st + 3)>(a[0], a[1], a[2], a[3]);
+                    static_for<4>([&](auto H) {
+                        constexpr int sp = st + decltype(H)::value, mt = sp & 15, kc = sp >> 4;
+                        o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[decltype(H)::value], pk[kc], o[mt], 0, 0, 0);
+                    });
+                    static_for<4>([&](auto H) {
+                        constexpr int n = st + decltype(H)::value + DEPTH;
+                        if constexpr (n < 32) vring[(st + decltype(H)::value) % DEPTH] = vread(std::integral_constant<int, n>{});
+                    });
                 });
             }
             __builtin_amdgcn_s_waitcnt(0);
