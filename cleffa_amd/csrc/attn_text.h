@@ -570,7 +570,8 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                 float mx = -INFINITY;
 #pragma unroll
                 for (int kt = 0; kt < 4; kt++)
-                    mx = fmaxf(fmaxf(mx, fmaxf(s[kt][0], s[kt][1])), fmaxf(s[kt][2], s[kt][3]));
+                    mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(s[kt][0], s[kt][1])),
+                                                       __builtin_elementwise_maximum(s[kt][2], s[kt][3]));
                 float alpha = 1.f;
                 if (__any(mx > 8.f || m_run == -INFINITY)) {
                     const float rmx = xrow_max(mx);
