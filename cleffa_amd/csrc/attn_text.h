@@ -267,17 +267,19 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(e) : "s"(p.blocks + 8 * (item_base(it) / p.nh)) : "memory");
         return decode_from(e, it);
     };
+    // Each fill is a uniform base plus a 32-bit per-lane offset, widened at the use (the empty asm
+    // keeps it 32-bit there), so the load takes the scalar-base form with no 64-bit address math.
+    auto lds_fill = [&](const char *base, unsigned off, uint16_t *dst) {
+        asm volatile("" : "+v"(off));
+        __builtin_amdgcn_global_load_lds((const void *)(base + off), (lds_void *)dst, 16, 0, 0);
+    };
     auto load_tiles = [&](const Item &s, int kb, uint16_t *Ks, uint16_t *Vs) {
         const char *kt_base = (const char *)(s.kbase + (size_t)kb * HD);
         const char *vt_base = (const char *)(s.vbase + kb);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(kt_base + kfo[j]),
-                                             (lds_void *)(Ks + (wave_s * 4 + j) * 512), 16, 0, 0);
+        for (int j = 0; j < 4; j++) lds_fill(kt_base, kfo[j], Ks + (wave_s * 4 + j) * 512);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[j]),
-                                             (lds_void *)(Vs + (wave_s * 4 + j) * 512), 16, 0, 0);
+        for (int j = 0; j < 4; j++) lds_fill(vt_base, vfo[j], Vs + (wave_s * 4 + j) * 512);
     };
     // Q or gate rows of the block (128 x 256 bf16 = 64 KB, `off` 0 or HD within the head's
     // 2*HD columns): rows 0-63 into G0, 64-127 into G1, slot s of a half = row s/32, 16-byte
@@ -297,8 +299,9 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             const int c = (ln & 31) ^ (row & 15);
             int rc = min(r0w + (row & 15), s.nq - 1);
             uint16_t *dst = (grp < 32 ? G0 : G1) + (grp & 31) * 512;
-            __builtin_amdgcn_global_load_lds((const void *)(p.qkv + ((size_t)s.q_row0 + rc) * p.row + (size_t)hw * 2 * HD + off + c * 8),
-                                             (lds_void *)dst, 16, 0, 0);
+            // the block's rows lie within 128 rows of the head's first: a 32-bit offset
+            const char *base = (const char *)(p.qkv + (size_t)s.q_row0 * p.row + (size_t)hw * 2 * HD + off);
+            lds_fill(base, (unsigned)(rc * p.row + c * 8) * 2u, dst);
         }
     };
     // the row's rotary cos/sin, written by the K/V prologue for this pass row
