@@ -39,6 +39,7 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
     using text::s_row_key;
     using text::lds_read16;
     using text::lds_wait;
+    using text::lds_wait2;
     using text::lds_addr;
     using text::static_for;
     using text::xrow_max;
@@ -80,18 +81,20 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
         const int d = vs >> 3, c = (vs & 7) ^ text::v_swz(d);
         vfo[j] = (unsigned)d * (unsigned)p.kvT * 2u + (unsigned)c * 16u;
     }
+    // a uniform base plus a 32-bit lane offset widened at the use (the empty asm keeps it 32-bit
+    // there): the scalar-base form of the load, no 64-bit address math
+    auto lds_fill = [&](const char *base, unsigned off, uint16_t *dst) {
+        asm volatile("" : "+v"(off));
+        __builtin_amdgcn_global_load_lds((const void *)(base + off), (lds_void *)dst, 16, 0, 0);
+    };
     auto load_tiles = [&](int kb, uint16_t *Ks, uint16_t *Vs) {
         const char *kt_base = (const char *)(kbase + (size_t)kb * HD);
         const char *vt_base = (const char *)(vbase + kb);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(kt_base + kfo[j]),
-                                             (lds_void *)(Ks + (wave_s * 4 + j) * 512), 16, 0, 0);
+        for (int j = 0; j < 4; j++) lds_fill(kt_base, kfo[j], Ks + (wave_s * 4 + j) * 512);
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-            __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[j]), (lds_void *)(Vs + (wave_s * 2 + j) * 512), 16, 0, 0);
-        if (wave_s == 0)
-            __builtin_amdgcn_global_load_lds((const void *)(vt_base + vfo[2]), (lds_void *)(Vs + 8 * 512), 16, 0, 0);
+        for (int j = 0; j < 2; j++) lds_fill(vt_base, vfo[j], Vs + (wave_s * 2 + j) * 512);
+        if (wave_s == 0) lds_fill(vt_base, vfo[2], Vs + 8 * 512);
     };
     auto zero_tail = [&](int kb, uint16_t *Vs) {   // V^T entries of keys >= k_len -> 0
         const int valid = k_len - kb;
@@ -194,21 +197,27 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
             });
             const float ms0 = m_run[0] == -INFINITY ? 0.f : m_run[0];
             const float ms1 = m_run[1] == -INFINITY ? 0.f : m_run[1];
-            static_for<QK>([&](auto I) {   // one K operand, both halves' products
-                constexpr int st = decltype(I)::value, kt = st & 3, c = st >> 2;
-                constexpr int ahead = (QK - 1 - st) < (DEPTH - 1) ? (QK - 1 - st) : (DEPTH - 1);
-                bf16x8 a = ring[st % DEPTH];
-                lds_wait<ahead>(a);
-                if constexpr (c == 0) {
-                    s[0][kt] = f32x4{-ms0, -ms0, -ms0, -ms0};
-                    s[1][kt] = f32x4{-ms1, -ms1, -ms1, -ms1};
-                }
-                s[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][c], s[0][kt], 0, 0, 0);
-                s[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][c], s[1][kt], 0, 0, 0);
-                if constexpr (st + DEPTH < QK) {
-                    constexpr int n = st + DEPTH, nkt = n & 3, nc = n >> 2;
-                    ring[st % DEPTH] = lds_read16<buf * 2 * KTILE>(ka[nkt][nc]);
-                }
+            // one K operand, both halves' products; operands waited for two at a time (one
+            // s_waitcnt per four products)
+            static_for<QK / 2>([&](auto P) {
+                constexpr int st = 2 * decltype(P)::value;
+                constexpr int last = (st + DEPTH - 1) < (QK - 1) ? (st + DEPTH - 1) : (QK - 1);
+                bf16x8 a2[2] = {ring[st % DEPTH], ring[(st + 1) % DEPTH]};
+                lds_wait2<last - (st + 1)>(a2[0], a2[1]);
+                static_for<2>([&](auto H) {
+                    constexpr int sp = st + decltype(H)::value, kt = sp & 3, c = sp >> 2;
+                    bf16x8 a = a2[decltype(H)::value];
+                    if constexpr (c == 0) {
+                        s[0][kt] = f32x4{-ms0, -ms0, -ms0, -ms0};
+                        s[1][kt] = f32x4{-ms1, -ms1, -ms1, -ms1};
+                    }
+                    s[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][c], s[0][kt], 0, 0, 0);
+                    s[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][c], s[1][kt], 0, 0, 0);
+                });
+                static_for<2>([&](auto H) {
+                    constexpr int n = st + decltype(H)::value + DEPTH, nkt = n & 3, nc = n >> 2;
+                    if constexpr (n < QK) ring[(st + decltype(H)::value) % DEPTH] = lds_read16<buf * 2 * KTILE>(ka[nkt][nc]);
+                });
             });
             constexpr int PV = NM * 2;
             auto vread = [&](auto I) {   // step st = NM * kc + mt
@@ -237,7 +246,8 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
                 float mx = -INFINITY;
 #pragma unroll
                 for (int kt = 0; kt < 4; kt++)
-                    mx = fmaxf(fmaxf(mx, fmaxf(s[hh][kt][0], s[hh][kt][1])), fmaxf(s[hh][kt][2], s[hh][kt][3]));
+                    mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(s[hh][kt][0], s[hh][kt][1])),
+                                                       __builtin_elementwise_maximum(s[hh][kt][2], s[hh][kt][3]));
                 // s holds score - running max. The max moves only when a tile's max passes it by
                 // more than 8 (log2 units), or on the first tile: P stays below 2^8, and the
                 // shift and the O rescale below run on few tiles. The lane's own max decides
@@ -265,14 +275,21 @@ __global__ __launch_bounds__(256, 2) void attn_vis_kernel(AttnParams p) {
                     pk[hh][kc] = __builtin_bit_cast(bf16x8, wv);
                 }
             }
-            static_for<PV>([&](auto I) {   // one V^T operand, both halves' products
-                constexpr int st = decltype(I)::value, mt = st % NM, kc = st / NM;
-                constexpr int ahead = (PV - 1 - st) < (DEPTH - 1) ? (PV - 1 - st) : (DEPTH - 1);
-                bf16x8 a = vring[st % DEPTH];
-                lds_wait<ahead>(a);
-                o[0][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[0][kc], o[0][mt], 0, 0, 0);
-                o[1][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[1][kc], o[1][mt], 0, 0, 0);
-                if constexpr (st + DEPTH < PV) vring[st % DEPTH] = vread(std::integral_constant<int, st + DEPTH>{});
+            static_for<PV / 2>([&](auto P) {   // one V^T operand, both halves' products, waited in pairs
+                constexpr int st = 2 * decltype(P)::value;
+                constexpr int last = (st + DEPTH - 1) < (PV - 1) ? (st + DEPTH - 1) : (PV - 1);
+                bf16x8 a2[2] = {vring[st % DEPTH], vring[(st + 1) % DEPTH]};
+                lds_wait2<last - (st + 1)>(a2[0], a2[1]);
+                static_for<2>([&](auto H) {
+                    constexpr int sp = st + decltype(H)::value, mt = sp % NM, kc = sp / NM;
+                    bf16x8 a = a2[decltype(H)::value];
+                    o[0][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[0][kc], o[0][mt], 0, 0, 0);
+                    o[1][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk[1][kc], o[1][mt], 0, 0, 0);
+                });
+                static_for<2>([&](auto H) {
+                    constexpr int n = st + decltype(H)::value + DEPTH;
+                    if constexpr (n < PV) vring[(st + decltype(H)::value) % DEPTH] = vread(std::integral_constant<int, n>{});
+                });
             });
         }
         __builtin_amdgcn_s_waitcnt(0);
