@@ -7,7 +7,7 @@
 //
 // Workgroup: 8 wavefronts (2 per SIMD), one block of 128 query rows of one q head per work item;
 // wave w owns rows 16w .. 16w+15. The state per wave (O^T 64, Q 32, S 16 VGPRs, operand rings,
-// addresses) fits 244 VGPRs, so two waves share a SIMD.
+// addresses) fits 237 VGPRs, so two waves share a SIMD.
 //   S^T = K . Q^T      v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K from LDS,
 //                      B = the wave's Q (registers). A lane owns one query column. Q and K are
 //                      f16: their 11-bit significands keep the scores of sharp rows within the
