@@ -327,7 +327,8 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     // and rotates them while the tile lands.
     int par = 0;
     {
-        const float qn_v = (p.q_norm && tid < HD) ? p.q_norm[tid] : 0.f;
+        // q_norm weights staged with the score scale (scale * log2 e) folded in
+        const float qn_v = (p.q_norm && tid < HD) ? p.q_norm[tid] * p.scale_log2 : 0.f;
         load_rows(cur, k1s, v1s, 0);
         load_cs(cur);
         if (cur.n_tiles > 0) load_tiles(cur, 0, k0s, v0s);
@@ -451,12 +452,12 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             // magnitude's bits, which order NaN above every number) and clamped.
             const float sc = p.scale_log2;
             bool q_bad;
-            if (p.q_norm) {
+            if (p.q_norm) {   // the scale came in with the staged weights
                 q_bad = !(ss <= 3.0e38f);
 #pragma unroll
                 for (int c = 0; c < NC; c++) {
-                    u32x4 w = {pack_f16(x[c][0] * sc, x[c][1] * sc), pack_f16(x[c][2] * sc, x[c][3] * sc),
-                               pack_f16(x[c][4] * sc, x[c][5] * sc), pack_f16(x[c][6] * sc, x[c][7] * sc)};
+                    u32x4 w = {pack_f16(x[c][0], x[c][1]), pack_f16(x[c][2], x[c][3]),
+                               pack_f16(x[c][4], x[c][5]), pack_f16(x[c][6], x[c][7])};
                     qf[c] = __builtin_bit_cast(f16x8, w);
                 }
             } else {
@@ -673,19 +674,24 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                 float v[8];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    v[i] = o[2 * u][i] * il;
-                    v[4 + i] = o[2 * u + 1][i] * il;
+                    v[i] = o[2 * u][i];
+                    v[4 + i] = o[2 * u + 1][i];
                 }
                 if (p.gate) {
                     if constexpr ((u & 1) == 0)
                         asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
                                      : "=&v"(gq[0]), "=&v"(gq[1]) : "v"(gaddr(u)), "v"(gaddr(u + 1)) : "memory");
                     const u32x4 gw = gq[u & 1];
+                    // O / l * sigmoid(g) = O / (l + l * 2^(-g log2 e)): one reciprocal per element
+                    // (a row's l is at least 1: its own key's P is 2^0 at the running max)
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
-                        v[2 * j] *= sigmoidf(bf_lo(gw[j]));
-                        v[2 * j + 1] *= sigmoidf(bf_hi(gw[j]));
+                        v[2 * j] *= __builtin_amdgcn_rcpf(fmaf(l_row, __builtin_amdgcn_exp2f(-bf_lo(gw[j]) * 1.4426950408889634f), l_row));
+                        v[2 * j + 1] *= __builtin_amdgcn_rcpf(fmaf(l_row, __builtin_amdgcn_exp2f(-bf_hi(gw[j]) * 1.4426950408889634f), l_row));
                     }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] *= il;
                 }
                 store_out8(p.out, t * p.out_ld + (size_t)h * HD + d0, v, p.out_type, p.f16_lim, flag);
             });
