@@ -7,7 +7,7 @@
 //
 // Workgroup: 8 wavefronts (2 per SIMD), one block of 128 query rows of one q head per work item;
 // wave w owns rows 16w .. 16w+15. The state per wave (O^T 64, Q 32, S 16 VGPRs, operand rings,
-// addresses) fits 237 VGPRs, so two waves share a SIMD.
+// addresses) fits 215 VGPRs, so two waves share a SIMD.
 //   S^T = K . Q^T      v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K from LDS,
 //                      B = the wave's Q (registers). A lane owns one query column. Q and K are
 //                      f16: their 11-bit significands keep the scores of sharp rows within the
@@ -306,12 +306,15 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     };
     // the row's rotary cos/sin, written by the K/V prologue for this pass row
     float4 csv[R > 0 ? R : 1][4];
+    // Loaded unconditionally (without a table, from the pass's own qkv rows, and not used): a load
+    // under a branch made the compiler reshuffle the registers inside it, right after the loads,
+    // waiting for them there.
     auto load_cs = [&](const Item &s) {
-        if (NROT > 0 && p.rope_cs) {
+        if (NROT > 0) {
             const int jw = wave_s / s.wph;
             const int my_q = (wave_s - jw * s.wph) * ROWS + q16;
             const size_t qrow = (size_t)s.q_row0 + (my_q < s.nq ? my_q : 0);
-            const float *cs = p.rope_cs + qrow * (NROT / 2) * 2;
+            const float *cs = p.rope_cs ? p.rope_cs + qrow * (NROT / 2) * 2 : (const float *)p.qkv;
 #pragma unroll
             for (int c = 0; c < R; c++)
 #pragma unroll
@@ -330,7 +333,6 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         // q_norm weights staged with the score scale (scale * log2 e) folded in
         const float qn_v = (p.q_norm && tid < HD) ? p.q_norm[tid] * p.scale_log2 : 0.f;
         load_rows(cur, k1s, v1s, 0);
-        load_cs(cur);
         if (cur.n_tiles > 0) load_tiles(cur, 0, k0s, v0s);
         // The LDS store of q_norm is issued as asm: the compiler would otherwise wait for the
         // tile's global_load_lds fills (vmcnt(0)) before touching LDS.
@@ -357,6 +359,10 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         const int wave_last_pos = cur.q_pos0 + row0w + ROWS - 1;
         const int k_len = cur.k_len, n_tiles = cur.n_tiles;
 
+        // The rotary cos/sin load here, at the item's start: they are first needed after the
+        // normalisation, and loaded in the previous item's epilogue, the compiler's moves of
+        // their registers at the loop's back edge waited there for the Q-row fills just issued.
+        load_cs(cur);
         // ---- Q prologue: lane holds Q[my_q][c*32 + 8g + j], the B operand of chunk c.
         f16x8 qf[NC];
         const int nxt = items.get(k + 1);
@@ -652,7 +658,6 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             cur = decode_from(ne, item);
             if (last_buf) load_rows(cur, k1s, v1s, 0);
             else load_rows(cur, k0s, v0s, 0);
-            load_cs(cur);
         }
         if (q_valid) {
             const float il = l_row > 0.f ? 1.f / l_row : 0.f;
