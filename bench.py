@@ -335,7 +335,7 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                          "(sharding is described in DESIGN.md, not launched)"}))
+                          "(the path would shard by records or kv heads; no multi-GPU run is launched)"}))
         sys.exit(2)
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
