@@ -12,7 +12,7 @@ SOURCES = [ROOT / "csrc" / "attn_api.hip", ROOT / "csrc" / "prefix_cache.hip", R
 BENCH_LIB = ROOT / "libclef_hip_bench.so"
 BENCH_SOURCES = [ROOT / "csrc" / "mfma_ceiling.hip"]
 DEPS = SOURCES + BENCH_SOURCES + [ROOT / "csrc" / "attn_kernels.h", ROOT / "csrc" / "attn_params.h", ROOT / "csrc" / "attn_text.h",
-                  ROOT / "csrc" / "attn_vis.h", ROOT / "csrc" / "omni_attn.h", ROOT / "csrc" / "attn_text_f32.h",
+                  ROOT / "csrc" / "attn_vis.h", ROOT / "csrc" / "omni_attn.h", ROOT / "csrc" / "attn_text_f32.h", ROOT / "csrc" / "gguf_view.h",
                   REPO / "include" / "clef_hip_attn.h"]
 
 

@@ -231,10 +231,11 @@ bool clef_hip_vis_attention_noalloc(const clef_hip_vis_args *a, void *stream, ch
 bool clef_hip_gemm(int T, int N, int K, const uint16_t *X, const uint16_t *W, void *Y, int y_type, int acc,
                    void *workspace, size_t ws_bytes, void *stream, char *err, size_t errlen);
 
-/* ---- The GEMMs' weights from the model file (clef_gguf.h / clef_gguf.c GGUF v3 reader; clef.c:27-59
- * load_config, 180-256 bind_weights). Host-only except the copies: a read-only view over an
- * mmap'd GGUF, every read bounds-checked (the file is untrusted), the attention geometry, and
- * one layer's attention tensors copied into device buffers the caller owns. */
+/* ---- The GEMMs' weights from the model file (replaces clef_gguf.h:52-63 gguf_open / find /
+ * get and clef.c:27-59 load_config, 180-256 bind_weights). Host-only except the copies: a
+ * read-only index over an mmap'd GGUF v3 file, every read bounds-checked (the file is untrusted),
+ * the attention geometry, and one layer's attention tensors copied into device buffers the
+ * caller owns. */
 #define CLEF_HIP_GGML_F32 0
 #define CLEF_HIP_GGML_F16 1
 #define CLEF_HIP_GGML_BF16 30
@@ -271,7 +272,8 @@ bool clef_hip_gguf_attn_config(const clef_hip_gguf *g, clef_hip_attn_config *c, 
  * rows [q | gate] per head, then K, then V: the QKV GEMM's W), blk.L.attn_output.weight BF16
  * [H][nh hd] (the o_proj's W), blk.L.attn_q_norm / attn_k_norm.weight F32 [hd] (already 1 + w).
  * Each is checked for type and shape, then copied on `stream` into the given device buffer
- * (NULL skips that tensor). */
+ * (NULL skips that tensor); the call waits for the stream before it returns, so the handle may
+ * be closed right after. */
 bool clef_hip_gguf_attn_layer(const clef_hip_gguf *g, const clef_hip_attn_config *c, int layer, uint16_t *w_qkv,
                               uint16_t *w_o, float *q_norm, float *k_norm, void *stream, char *err, size_t errlen);
 /* Vision tower layer `layer` (clef.c:291-294): v.blk.L.attn_qkv.weight BF16 [3E][E] and .bias F32 [3E],

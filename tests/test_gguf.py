@@ -225,3 +225,76 @@ def test_layer_binding_checks(tmp_path, model):
         c = g.attn_config()
         assert not lib.clef_hip_gguf_attn_layer(g._h, ctypes.byref(c), 0, None, None, None, None, None, err, 256)
         assert b"attn_q_norm.weight has type 30" in err.value
+
+
+def _raw_gguf(meta_blobs, tensor_blobs=b"", n_tensors=0, tail=b"\0" * 64):
+    """A GGUF from already-encoded metadata entries (key + type + value bytes) and tensor entries."""
+    import struct
+    return struct.pack("<IIQQ", 0x46554747, 3, n_tensors, len(meta_blobs)) + b"".join(meta_blobs) + tensor_blobs + tail
+
+
+def _entry(key, t, value_bytes):
+    import struct
+    k = key.encode()
+    return struct.pack("<Q", len(k)) + k + struct.pack("<I", t) + value_bytes
+
+
+def _arr(et, n, body=b""):
+    import struct
+    return struct.pack("<IQ", et, n) + body
+
+
+@pytest.mark.parametrize("case", ["str_depth1", "str_depth2", "str_depth3", "arr_depth3_scalars", "arr_depth3_strings",
+                                  "empty_bad_elem", "one_bad_elem", "bad_scalar_type", "align_i32", "align_u32_64",
+                                  "misaligned_offset", "overlap", "huge_count_scalars", "rank5", "zero_extent"])
+def test_edge_files_agree_with_reference(tmp_path, case):
+    """Hand-built files at the edges of the acceptance rules: array nesting (strings and arrays
+    inside at most two arrays), empty arrays of an unknown element type, an alignment key of the
+    wrong type, tensor offsets that are unaligned or overlap. Both readers decide alike and, where
+    they accept, give the same table."""
+    import struct
+    s = lambda x: struct.pack("<Q", len(x)) + x
+    strs = lambda *xs: b"".join(s(x) for x in xs)
+    tensor = lambda name, dims, t, off: s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims) + struct.pack("<IQ", t, off)
+    expect = None
+    meta, tens, nt = [], b"", 0
+    if case == "str_depth1":
+        meta = [_entry("a", 9, _arr(8, 2, strs(b"x", b"yy")))]; expect = True
+    elif case == "str_depth2":
+        meta = [_entry("a", 9, _arr(9, 1, _arr(8, 1, strs(b"x"))))]; expect = True
+    elif case == "str_depth3":
+        meta = [_entry("a", 9, _arr(9, 1, _arr(9, 1, _arr(8, 1, strs(b"x")))))]; expect = False
+    elif case == "arr_depth3_scalars":
+        meta = [_entry("a", 9, _arr(9, 1, _arr(9, 1, _arr(4, 2, b"\0" * 8))))]; expect = True
+    elif case == "arr_depth3_strings":
+        meta = [_entry("a", 9, _arr(9, 1, _arr(9, 1, _arr(9, 0))))]; expect = True
+    elif case == "empty_bad_elem":
+        meta = [_entry("a", 9, _arr(77, 0))]; expect = True
+    elif case == "one_bad_elem":
+        meta = [_entry("a", 9, _arr(77, 1, b"\0" * 8))]; expect = False
+    elif case == "bad_scalar_type":
+        meta = [_entry("a", 13, b"\0" * 8)]; expect = False
+    elif case == "align_i32":   # not a u32: the default 32 applies
+        meta = [_entry("general.alignment", 5, struct.pack("<i", 48))]; tens = tensor(b"t", [4], 0, 0); nt = 1; expect = True
+    elif case == "align_u32_64":
+        meta = [_entry("general.alignment", 4, struct.pack("<I", 64))]; tens = tensor(b"t", [4], 0, 0); nt = 1; expect = True
+    elif case == "misaligned_offset":
+        tens = tensor(b"t", [3], 30, 6) + tensor(b"u", [2], 0, 3); nt = 2; expect = True
+    elif case == "overlap":
+        tens = tensor(b"t", [8], 0, 0) + tensor(b"u", [8], 0, 4); nt = 2; expect = True
+    elif case == "huge_count_scalars":
+        meta = [_entry("a", 9, _arr(10, 1 << 61))]; expect = False
+    elif case == "rank5":
+        tens = tensor(b"t", [1, 1, 1, 1, 1], 0, 0); nt = 1; expect = False
+    elif case == "zero_extent":
+        tens = tensor(b"t", [4, 0], 0, 0); nt = 1; expect = False
+    p = tmp_path / "e.gguf"
+    p.write_bytes(_raw_gguf(meta, tens, nt, tail=b"\0" * 256))
+    ok_o, ours = _our_table(p)
+    assert ok_o == expect
+    lib = _ref_lib()
+    if lib is not None:
+        ok_r, ref = _ref_table(lib, p)
+        assert ok_r == ok_o
+        if ok_o:
+            assert ours == ref
