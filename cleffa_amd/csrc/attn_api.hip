@@ -26,6 +26,19 @@ namespace {
 
 constexpr int kVersion = 4;
 constexpr int32_t kSchedMagic = 0x53434844;   // header word of a schedule ('SCHD')
+constexpr int kSchedHeader = 8;                 // {magic, n_blk, nh, n_wg, nkv, fingerprint, 0, 0}
+// A 32-bit fingerprint of a block list: FNV-1a over words 0-6 of every entry (word 7 holds the
+// fingerprint itself), never 0. The plan stores it in word 7 of every entry and the schedule in
+// its header, so the kernel can tell whether a schedule was built for the plan it runs.
+int32_t blocks_fingerprint(const int32_t *blocks, int n_blk) {
+    uint32_t h = 2166136261u;
+    for (int b = 0; b < n_blk; b++)
+        for (int i = 0; i < CLEF_HIP_BLOCK_INTS - 1; i++) {
+            const uint32_t w = (uint32_t)blocks[CLEF_HIP_BLOCK_INTS * b + i];
+            for (int k = 0; k < 4; k++) h = (h ^ ((w >> (8 * k)) & 0xffu)) * 16777619u;
+        }
+    return (int32_t)(h | 1u);
+}
 constexpr int kVisHD = 72;
 
 bool fail(char *err, size_t errlen, const char *fmt, ...) {
@@ -218,14 +231,18 @@ bool clef_hip_attn_init(char *err, size_t errlen) {
     if (prop.warpSize != 64) return fail(err, errlen, "attention kernels need 64-wide wavefronts (device reports %d)", prop.warpSize);
     const size_t need = sizeof(uint16_t) * text::LDS_ELEMS;
     if (prop.sharedMemPerBlock < need) return fail(err, errlen, "device LDS %zu < %zu bytes", (size_t)prop.sharedMemPerBlock, need);
-    char *scratch_ptr = nullptr;   // resolve this device's scratch address now, not on a first call
-    return scratch_base(&scratch_ptr, err, errlen);
+    // Resolve this device's scratch address now, not on a first call. A failure disables only
+    // clef_hip_vis_attention_noalloc, which tries again and reports it on each call.
+    char *scratch_ptr = nullptr;
+    char ignored[8];
+    (void)scratch_base(&scratch_ptr, ignored, sizeof(ignored));
+    return true;
 }
 
 int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg) {
     if (n_blk < 0 || nh <= 0 || n_wg <= 0) return 0;
     const long items = (long)n_blk * nh * (sched_splits(n_blk, nh, n_wg) ? 2 : 1);
-    return items + 5 + n_wg > 0x7fffffffL ? 0 : (int)(4 + n_wg + 1 + items);
+    return items + kSchedHeader + 1 + n_wg > 0x7fffffffL ? 0 : (int)(kSchedHeader + n_wg + 1 + items);
 }
 
 bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,
@@ -234,7 +251,7 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
         return fail(err, errlen, "bad schedule arguments");
     if ((long)n_blk * nh >= (1L << 28)) return fail(err, errlen, "too many items for a schedule");
     const bool split = sched_splits(n_blk, nh, n_wg);
-    const long need = 4L + n_wg + 1 + (long)n_blk * nh * (split ? 2 : 1);
+    const long need = (long)kSchedHeader + n_wg + 1 + (long)n_blk * nh * (split ? 2 : 1);
     if (need > max_sched) return fail(err, errlen, "schedule needs %ld entries, room for %d", need, max_sched);
     // cost of an item in 64-key tiles: its tiles plus the prologue / epilogue (Q rows, gate,
     // output stores). Measured at about three tiles' time per item, but a weight of 6 balances
@@ -338,7 +355,10 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
     sched[1] = n_blk;
     sched[2] = nh;
     sched[3] = n_wg;
-    int32_t *const offs = sched + 4;
+    sched[4] = nkv;
+    sched[5] = blocks_fingerprint(blocks, n_blk);
+    sched[6] = sched[7] = 0;
+    int32_t *const offs = sched + kSchedHeader;
     int off = 0;
     for (int b = 0; b < n_wg; b++) {
         offs[b] = off;
@@ -411,6 +431,8 @@ bool clef_hip_attn_plan(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int
     // orders each record's blocks longest first; here the order is global across records).
     std::stable_sort(ents.begin(), ents.end(), [](const Ent &x, const Ent &y) { return x.v[4] > y.v[4]; });
     for (size_t i = 0; i < ents.size(); i++) memcpy(blocks + CLEF_HIP_BLOCK_INTS * i, ents[i].v, sizeof(ents[i].v));
+    const int32_t fp = blocks_fingerprint(blocks, (int)ents.size());
+    for (size_t i = 0; i < ents.size(); i++) blocks[CLEF_HIP_BLOCK_INTS * i + 7] = fp;
     kv_off = 0;
     for (int r = 0; r < n_seq; r++) {
         const int nq = cu_q[r + 1] - cu_q[r];

@@ -200,9 +200,10 @@ __global__ __launch_bounds__(16 * kPrepRows) void text_prep_kv_kernel(PrepParams
             wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
         }
     }
-    // A non-finite V element (bf16 exponent all ones) saturates to +-65536 (bf16's rounding of
-    // 65504) and flags the record, as split16 does for the reference's f16 V plane
-    // (metal/clef.metal:857-867): nothing past a record's own keys can then read inf or NaN.
+    // A V element with |v| > f16_lim, or NaN, saturates to +-65536 (bf16's rounding of 65504)
+    // and flags the record, as split16 does for the reference's f16 V plane
+    // (metal/clef.metal:857-867): the same records are flagged for the FP32 rerun, and nothing
+    // past a record's own keys can read inf or NaN.
     bool bad = false;
 #pragma unroll
     for (int h = 0; h < 2; h++)
@@ -210,7 +211,8 @@ __global__ __launch_bounds__(16 * kPrepRows) void text_prep_kv_kernel(PrepParams
         for (int j = 0; j < 4; j++) {
             kw[h][j] = t >= 0 ? kw[h][j] : 0u;
             unsigned w = t >= 0 ? vw[h][j] : 0u;
-            const bool lo_bad = (w & 0x7f80u) == 0x7f80u, hi_bad = (w & 0x7f800000u) == 0x7f800000u;
+            const bool lo_bad = !(__uint_as_float((w & 0x7fffu) << 16) <= p.f16_lim),
+                       hi_bad = !(__uint_as_float(w & 0x7fff0000u) <= p.f16_lim);
             if (lo_bad) w = (w & 0xffff8000u) | 0x4780u;
             if (hi_bad) w = (w & 0x8000ffffu) | 0x47800000u;
             bad |= lo_bad | hi_bad;

@@ -24,7 +24,7 @@ struct AttnParams {
     int n_blk;                // blocks in the plan (work items = n_blk * nh)
     int xcd_heads;            // nh / 8 when heads split evenly over the 8 XCDs, else 0
     uint64_t *trace;          // NULL, or [n_blk * nh][8] per work item: start, end, HW_ID, XCC_ID, prologue end, loop end, workgroup, ordinal
-    const int32_t *sched;     // NULL, or a schedule: header {magic, n_blk, nh, n_wg}, [n_wg + 1] offsets, items
+    const int32_t *sched;     // NULL, or a schedule: header {magic, n_blk, nh, n_wg, nkv, fingerprint, 0, 0}, [n_wg + 1] offsets, items
 };
 
 struct PrepParams {

@@ -151,12 +151,20 @@ struct ItemList {
         per_x = xh ? p.n_blk * xh : 0;
         list = nullptr;
         s0 = s1 = 0;
-        // a schedule: header {magic, n_blk, nh, n_wg}, then offsets and items
+        // A schedule: header {magic, n_blk, nh, n_wg, nkv, fingerprint, 0, 0}, then offsets and
+        // items. It is used only when the header names this pass: its sizes, this grid, and the
+        // fingerprint the plan wrote into word 7 of every block entry. Otherwise every
+        // workgroup (all read the same words) takes the static order, which covers every item.
         if (p.sched) {
-            const int32_t *offs = p.sched + 4;
-            s0 = sload(offs + blockIdx.x);
-            s1 = sload(offs + blockIdx.x + 1);
-            list = offs + gridDim.x + 1;
+            i32x8 h;
+            asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(h) : "s"(p.sched) : "memory");
+            const int fp = sload(p.blocks + 7);
+            if (h[0] == 0x53434844 && h[1] == p.n_blk && h[2] == p.nh && h[3] == (int)gridDim.x && h[4] == p.nkv && h[5] == fp) {
+                const int32_t *offs = p.sched + 8;
+                s0 = sload(offs + blockIdx.x);
+                s1 = sload(offs + blockIdx.x + 1);
+                list = offs + gridDim.x + 1;
+            }
         }
     }
     // the k-th item of this workgroup (block * nh + head, with the rows code above), or -1
@@ -331,13 +339,20 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     int par = 0;
     {
         // q_norm weights staged with the score scale (scale * log2 e) folded in
-        const float qn_v = (p.q_norm && tid < HD) ? p.q_norm[tid] * p.scale_log2 : 0.f;
+        const float qn_w = (p.q_norm && tid < HD) ? p.q_norm[tid] : 0.f;
+        const float qn_v = qn_w * p.scale_log2;
+        // A normalised, rotated element is at most 16 max|w| (|x_i| / rms <= sqrt(HD) = 16, and
+        // the rotation keeps a pair's norm): only weights past f16_lim / 16 (or NaN) can take an
+        // element past f16_lim. Each wave stores whether it holds one, after q_norm.
+        const int wide = __any(!(fabsf(qn_w) * 16.f <= p.f16_lim)) ? 1 : 0;
         load_rows(cur, k1s, v1s, 0);
         if (cur.n_tiles > 0) load_tiles(cur, 0, k0s, v0s);
-        // The LDS store of q_norm is issued as asm: the compiler would otherwise wait for the
-        // tile's global_load_lds fills (vmcnt(0)) before touching LDS.
+        // The LDS stores are issued as asm: the compiler would otherwise wait for the tile's
+        // global_load_lds fills (vmcnt(0)) before touching LDS.
         if (tid < HD) asm volatile("ds_write_b32 %0, %1" : : "v"(qn_addr + 4u * tid), "v"(qn_v) : "memory");
+        if (lane == 0) asm volatile("ds_write_b32 %0, %1" : : "v"(qn_addr + 4u * (HD + wave)), "v"(wide) : "memory");
     }
+    int wide_w = 0;   // some q_norm weight can leave f16's range: check the Q operands elementwise
 
     for (int k = 0;; k++) {
         // trace row of this item (100 MHz wall clock): start, end, HW_ID, XCC_ID, prologue end,
@@ -394,6 +409,12 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
                 for (int j = 0; j < 8; j++) ss += x[c][j] * x[c][j];
             }
             ss = xrow_sum(ss);
+            if (p.q_norm && k == 0) {   // the waves' wide-weight words, once per workgroup
+                u32x4 f0, f1;
+                asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
+                             : "=&v"(f0), "=&v"(f1) : "v"(qn_addr + 4u * HD) : "memory");
+                wide_w = __builtin_amdgcn_readfirstlane((int)(f0[0] | f0[1] | f0[2] | f0[3] | f1[0] | f1[1] | f1[2] | f1[3]));
+            }
             if (p.q_norm) {   // NULL: no q/k norm (plain SDPA operands)
                 const float inv = rsqrtf(ss / (float)HD + p.eps);
 #pragma unroll
@@ -453,20 +474,13 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             // Scaled by scale * log2 e before the one rounding to f16: the products give scores in
             // the exp2 domain. The f16 operand follows split16 (metal/clef.metal:857-867): an
             // element with |q| > f16_lim or NaN flags the record, and the operand saturates.
-            // Normalised rows are bounded by 16 max|w|; only a row that is not finite (its sum of
-            // squares) can flag. Plain rows are checked element by element (the largest
-            // magnitude's bits, which order NaN above every number) and clamped.
+            // Normalised rows are bounded by 16 max|w|: unless a weight is that large, only a row
+            // that is not finite (its sum of squares) can flag, and only then do the wave's rows
+            // take the elementwise check. Plain rows are always checked element by element (the
+            // largest magnitude's bits, which order NaN above every number) and clamped.
             const float sc = p.scale_log2;
             bool q_bad;
-            if (p.q_norm) {   // the scale came in with the staged weights
-                q_bad = !(ss <= 3.0e38f);
-#pragma unroll
-                for (int c = 0; c < NC; c++) {
-                    u32x4 w = {pack_f16(x[c][0], x[c][1]), pack_f16(x[c][2], x[c][3]),
-                               pack_f16(x[c][4], x[c][5]), pack_f16(x[c][6], x[c][7])};
-                    qf[c] = __builtin_bit_cast(f16x8, w);
-                }
-            } else {
+            auto pack_checked = [&](const float mul, const float lim) {
                 unsigned amax = 0;
 #pragma unroll
                 for (int c = 0; c < NC; c++) {
@@ -474,12 +488,27 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
                         amax = max(amax, __float_as_uint(x[c][j]) & 0x7fffffffu);
-                        y[j] = __builtin_amdgcn_fmed3f(x[c][j] * sc, -65504.f, 65504.f);
+                        y[j] = __builtin_amdgcn_fmed3f(x[c][j] * mul, -65504.f, 65504.f);
                     }
                     u32x4 w = {pack_f16(y[0], y[1]), pack_f16(y[2], y[3]), pack_f16(y[4], y[5]), pack_f16(y[6], y[7])};
                     qf[c] = __builtin_bit_cast(f16x8, w);
                 }
-                q_bad = amax > __float_as_uint(p.f16_lim);
+                return amax > __float_as_uint(lim);
+            };
+            if (p.q_norm) {   // the scale came in with the staged weights
+                q_bad = !(ss <= 3.0e38f);
+                if (wide_w || __any(q_bad)) {
+                    q_bad = pack_checked(1.f, p.f16_lim * sc) || q_bad;
+                } else {
+#pragma unroll
+                    for (int c = 0; c < NC; c++) {
+                        u32x4 w = {pack_f16(x[c][0], x[c][1]), pack_f16(x[c][2], x[c][3]),
+                                   pack_f16(x[c][4], x[c][5]), pack_f16(x[c][6], x[c][7])};
+                        qf[c] = __builtin_bit_cast(f16x8, w);
+                    }
+                }
+            } else {
+                q_bad = pack_checked(sc, p.f16_lim);
             }
             if (q_bad && q_valid && p.ovf)
                 __hip_atomic_store(p.ovf + cur.flag_row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -652,7 +681,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         const float l_row = xrow_sum(l_run);   // outside the row-divergent branch: lanes exchange values
         const int last_buf = (par + n_tiles + 1) & 1;
         const int gate_buf = last_buf ^ 1;
-        const int q_row0 = cur.q_row0, flag_row = cur.flag_row, h = my_h;
+        const int q_row0 = cur.q_row0, flag_row = cur.flag_row, h = my_h, hk_done = cur.hk;
         item = nxt;
         if (item >= 0) {
             cur = decode_from(ne, item);
@@ -711,7 +740,12 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
             }
             par = gate_buf;
         }
-        if (tr) tr[1] = wall_clock64();
+        if (tr) {
+            tr[1] = wall_clock64();
+            // the other heads of a packed item get the same row
+            for (int j = 1; j < hk_done; j++)
+                for (int i = 0; i < 8; i++) tr[8 * j + i] = tr[i];
+        }
         if (item < 0) break;
     }
 }
@@ -721,7 +755,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
 template <int NROT>
 __global__ __launch_bounds__(512, 1) void attn_text_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t smem[text::LDS_ELEMS];
-    __shared__ __attribute__((aligned(16))) float qn_lds[text::HD];
+    __shared__ __attribute__((aligned(16))) float qn_lds[text::HD + 8];   // q_norm, then a word per wave
     text_items<NROT>(p, smem, qn_lds);
 }
 

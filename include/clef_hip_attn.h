@@ -67,7 +67,9 @@ int clef_hip_attn_plan_max_blocks(int n_seq, int Tq);
  * (clef_gpu_forward_prefix, clef_metal.m:1640-1666): record r's keys occupy kv rows
  * cu_k[r] .. cu_k[r+1] (multiples of 8), its first cu_k[r+1]-cu_k[r]-(cu_q[r+1]-cu_q[r]) keys are
  * cached, and its queries are the last tokens. causal = 0 gives bidirectional attention within
- * each record (vision). Outputs: blocks [max_blocks][8] (sorted longest first), tok_kv
+ * each record (vision). Outputs: blocks [max_blocks][8] (sorted longest first; an entry is
+ * {q_row0, nq, q_pos0, k_row0, k_len, record's first pass row, record, fingerprint}, the last a
+ * 32-bit hash of words 0-6 of all entries, the same in each, that ties a schedule to the plan), tok_kv
  * [max_tok >= cu_q[n_seq]] (the K/V plane row each pass row's key lands in), kv_tok
  * [max_kv >= *kv_rows] (the inverse: the pass row whose key each plane row takes, -1 for rows
  * the pass does not write; NULL skips it), *n_blk, *kv_rows (rows per head the K and V^T
@@ -115,21 +117,23 @@ typedef struct {
                                  a key or query element with |x| > f16_lim or NaN is saturated to
                                  +-65504 and flags its record, as split16 does
                                  (metal/clef.metal:857-867); so does an f16 output (act16) with
-                                 CLEF_HIP_OUT_F16. Non-finite V elements (V is bf16 here) are
-                                 saturated to +-65504 and flag too */
+                                 CLEF_HIP_OUT_F16. V elements (bf16 here) with |v| > f16_lim
+                                 or NaN are saturated to +-65536 and flag too */
     int32_t *ovf;             /* [T] int32 flags, set at the record's first pass row; may be NULL */
     uint64_t *trace;          /* NULL, or [n_blk * nh][8] u64 per work item (query block, q head;
                                  of a block split in halves by the schedule, the first half):
                                  start, end (100 MHz device wall clock), HW_ID and XCC_ID
                                  registers, end of the prologue, end of the key loop, workgroup,
                                  ordinal in the workgroup; the CLEF_PROFILE analogue
-                                 (clef_metal.m:52-68) at work-item grain */
+                                 (clef_metal.m:52-68) at work-item grain. The heads of an item
+                                 that runs several heads of a short block get the same row */
     const int32_t *sched;     /* NULL, or device copy of clef_hip_attn_schedule's output for this
-                                 plan, nh and n_wg: the core then runs n_wg workgroups, each
-                                 over its own item list. A list built for another plan, nh or
-                                 n_wg gives undefined output (its header names the (n_blk, nh,
-                                 n_wg) it was built for); the kernel never runs an item index
-                                 outside this plan, so it cannot reach memory outside it */
+                                 plan, nh, nkv and n_wg: the core then runs n_wg workgroups, each
+                                 over its own item list. The kernel checks the list's header
+                                 against the call (n_blk, nh, nkv, n_wg) and against the plan
+                                 fingerprint in word 7 of the block entries; a list built for
+                                 another plan or shape is not used, and the n_wg workgroups run
+                                 the static order instead (the same output, unbalanced) */
     int n_wg;
     const int32_t *seq_start; /* [T] device int32: each pass row's record start (the reference's
                                  seq_start, clef_engine.h:179), where prep_kv flags a key that
@@ -155,7 +159,8 @@ typedef struct {
  * (cost: the block's 64-key tiles plus a fixed per-item cost), within the workgroups of the XCD
  * that owns the item's q head when the heads divide evenly over the 8 XCDs (workgroup b runs on
  * XCD b % 8). blocks: the plan's host block list. Output: a header {0x53434844, n_blk, nh,
- * n_wg}, then n_wg + 1 item offsets per workgroup, then the items, each workgroup's longest
+ * n_wg, nkv, fingerprint of the block list (the value clef_hip_attn_plan writes into word 7 of
+ * every block entry), 0, 0}, then n_wg + 1 item offsets per workgroup, then the items, each workgroup's longest
  * first. An item is block * nh + head in bits 0-27 and, in bits 28-29, what it runs: 0 the whole
  * block for that head; when the pass has fewer items than workgroups, a block of more than 64
  * rows becomes two items, 1 (rows 0-63) and 2 (rows 64-127), so that more workgroups have work;

@@ -281,3 +281,71 @@ def test_vision_f16_overflow_flags_isolated():
     for r in (0, 2, 3):
         x, y = int(cu[r]), int(cu[r + 1])
         assert torch.equal(_bits(out[x:y]), _bits(clean[x:y])), f"image {r} changed"
+
+
+def test_large_finite_value_flags_its_record():
+    """A finite V element past f16's range (1e5, exact in bf16's range) flags its record, as
+    split16 does for the reference's f16 V plane; the other records keep their bytes."""
+    _say("[split16] finite v overflow")
+    lengths = [100, 150, 64, 200]
+    w = workloads.text_inputs(lengths, 8, 2, n_rot=0, seed=14, norm=False, outlier_frac=0)
+    w.update(gate=True, theta=1e7)
+    cu = w["cu_seqlens"]
+    q = w["qkv"].clone()
+    r0 = int(cu[1])
+    q[r0 + 9, 2 * 8 * 256 + 2 * 256 + 17] = 1e5
+    ovf = torch.zeros(int(cu[-1]), dtype=torch.int32, device="cuda")
+    out, _ = gpu_text(dict(w, qkv=q), ovf=ovf)
+    clean, _ = gpu_text(w)
+    want = np.zeros(int(cu[-1]), np.int32)
+    want[r0] = 1
+    assert np.array_equal(ovf.cpu().numpy(), want)
+    assert torch.isfinite(out.float()).all()
+    for r in (0, 2, 3):
+        a, b = int(cu[r]), int(cu[r + 1])
+        assert torch.equal(_bits(out[a:b]), _bits(clean[a:b])), f"record {r} changed"
+
+
+@pytest.mark.parametrize("kind", ["inf_element", "wide_weights"])
+def test_normalised_query_overflow(kind):
+    """Normalised Q rows follow split16 too. An inf element in one query row (its sum of squares
+    is inf) flags only its record and leaves every output finite. q_norm weights large enough
+    that 16 max|w| passes f16's range switch the elementwise check on: with one weight of 1e6,
+    that dim's normalised element passes 65504 in most rows (|x / rms| > 0.066), so every record
+    is flagged."""
+    _say(f"[split16] normalised q {kind}")
+    lengths = [100, 150, 64, 200]
+    nh, nkv, hd = 8, 2, 256
+    w = workloads.text_inputs(lengths, nh, nkv, n_rot=64, seed=15, norm=True, outlier_frac=0)
+    w.update(gate=True, theta=1e7)
+    cu = w["cu_seqlens"]
+    T = int(cu[-1])
+    ovf = torch.zeros(T, dtype=torch.int32, device="cuda")
+    clean, _ = gpu_text(w)
+    if kind == "inf_element":
+        q = w["qkv"].clone()
+        r0 = int(cu[1])
+        q[r0 + 7, 2 * hd + 11] = float("inf")     # head 1's query, record 1
+        out, _ = gpu_text(dict(w, qkv=q), ovf=ovf)
+        want = np.zeros(T, np.int32)
+        want[r0] = 1
+        assert np.array_equal(ovf.cpu().numpy(), want), np.nonzero(ovf.cpu().numpy())
+        assert torch.isfinite(out.float()).all()
+        for r in (0, 2, 3):
+            a, b = int(cu[r]), int(cu[r + 1])
+            assert torch.equal(_bits(out[a:b]), _bits(clean[a:b])), f"record {r} changed"
+    else:
+        qn = w["q_norm"].clone()
+        qn[5] = 1e6
+        out, _ = gpu_text(dict(w, q_norm=qn), ovf=ovf)
+        flags = ovf.cpu().numpy()
+        want = np.zeros(T, np.int32)
+        want[np.asarray(cu[:-1])] = 1
+        assert np.array_equal(flags, want), np.nonzero(flags)
+        assert torch.isfinite(out.float()).all()
+        # weights below the bound (here 1,000: 16,000 < 65504) flag nothing and change no bits
+        # against a pass that takes the elementwise path only because of the bound
+        ovf.zero_()
+        qn[5] = 1000.0
+        gpu_text(dict(w, q_norm=qn), ovf=ovf)
+        assert not ovf.cpu().numpy().any()

@@ -106,3 +106,33 @@ def test_random_vision_pass(seed):
     out = vis.forward(qkv.cuda(), None if bias is None else bias.cuda(), torch.from_numpy(pos2).cuda(), plan)
     torch.cuda.synchronize()
     assert_close(out.float().cpu().numpy(), want, what=f"vision seed {seed}")
+
+
+@pytest.mark.parametrize("foreign", ["other_plan", "other_n_wg", "other_nkv"])
+def test_foreign_schedule_runs_static_order(foreign):
+    """A schedule built for another plan (same block count and heads, but short blocks that the
+    other plan packs several heads to an item), for another workgroup count, or for another kv
+    head count is refused by the kernel's header check: the pass runs the static order and gives
+    bitwise the output of a pass without a schedule."""
+    lengths, other = [40, 40, 200], [100, 100, 200]
+    nh, nkv, n_wg = 24, 4, 64
+    _say(f"[sweep] foreign schedule: {foreign}")
+    w = workloads.text_inputs(lengths, nh, nkv, n_rot=64, seed=3)
+    w.update(gate=True, theta=1e7)
+    att = TextAttention(nh, nkv, 256, 64, rope_theta=1e7)
+    plan = AttnPlan(w["cu_seqlens"], causal=True)
+    alien = AttnPlan(np.concatenate([[0], np.cumsum(other)]).astype(np.int32), causal=True)
+    assert alien.n_blk == plan.n_blk
+    if foreign == "other_plan":
+        plan.schedule = lambda nh_, nkv_, n: alien.schedule(nh_, nkv_, n)
+    elif foreign == "other_n_wg":
+        plan.schedule = lambda nh_, nkv_, n: AttnPlan.schedule(plan, nh_, nkv_, n + 8)
+    else:
+        plan.schedule = lambda nh_, nkv_, n: AttnPlan.schedule(plan, nh_, 2 * nkv_ if nkv_ < nh_ else nkv_, n)
+    d = lambda t: t.cuda()
+    args = (d(w["qkv"]), d(w["q_norm"]), d(w["k_norm"]), d(w["pos3"]), plan)
+    got = att.forward(*args, gate=True, schedule=n_wg)
+    whole = att.forward(*args, gate=True, schedule=False)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), whole.view(torch.int16))
+    assert_close(got.float().cpu().numpy(), oracle_text(w), what=f"foreign schedule {foreign}")

@@ -125,8 +125,11 @@ def test_schedule_covers_items_balanced(lengths, nh, nkv, n_wg):
     plan = AttnPlan(cu, causal=True, device="cpu")
     ok, s, err = _sched(plan, nh, nkv, n_wg)
     assert ok, err
-    assert s[:4].tolist() == [0x53434844, plan.n_blk, nh, n_wg]   # the header names the plan
-    s = s[4:]
+    # the header names the plan: its sizes and the fingerprint in word 7 of every block entry
+    fp = plan.blocks_host[:, 7]
+    assert plan.n_blk == 0 or (fp == fp[0]).all() and fp[0] != 0
+    assert s[:8].tolist() == [0x53434844, plan.n_blk, nh, n_wg, nkv, int(fp[0]) if plan.n_blk else s[5], 0, 0]
+    s = s[8:]
     off = s[: n_wg + 1]
     items = s[n_wg + 1: n_wg + 1 + off[-1]]
     split_pass = plan.n_blk * nh < n_wg
@@ -202,8 +205,36 @@ def test_schedule_local_search_reaches_c1_bound():
     plan = AttnPlan(cu, causal=True, device="cpu")
     ok, s, err = _sched(plan, 24, 4, 256)
     assert ok, err
-    off = s[4:261]
-    items = s[261:261 + off[-1]]
+    off = s[8:265]
+    items = s[265:265 + off[-1]]
     cost = lambda it: _item_cost(plan, 24, it)
     loads = [sum(cost(it) for it in items[off[b]:off[b + 1]]) for b in range(256)]
     assert sum(loads) == 10432 and max(loads) <= 42
+
+
+def _fnv_fingerprint(blocks):
+    """FNV-1a (32-bit, offset basis 2166136261, prime 16777619) over the little-endian bytes of
+    words 0-6 of every entry, with bit 0 forced on."""
+    h = 2166136261
+    for e in np.asarray(blocks, np.int32):
+        for byte in e[:7].astype("<i4").tobytes():
+            h = ((h ^ byte) * 16777619) & 0xFFFFFFFF
+    return np.int32(np.uint32(h | 1).view(np.int32))
+
+
+def test_plan_fingerprint():
+    """Word 7 of every block entry is the FNV-1a fingerprint of the list (textbook FNV-1a, written
+    out here); plans that differ in any block differ in it, and the schedule header repeats it."""
+    seen = set()
+    for lengths in ([1160, 890, 730, 425, 472, 136, 179, 104], [1160, 890, 730, 425, 472, 136, 180, 103],
+                    [100, 20], [20, 100], [300]):
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        plan = AttnPlan(cu, causal=True, device="cpu")
+        fp = _fnv_fingerprint(plan.blocks_host)
+        assert (plan.blocks_host[:, 7] == fp).all()
+        seen.add(int(fp))
+        ok, s, err = _sched(plan, 24, 4, 256)
+        assert ok and s[5] == fp and s[4] == 4
+    assert len(seen) == 5
+    # FNV-1a known answer: the empty input hashes to the offset basis
+    assert _fnv_fingerprint(np.zeros((0, 8), np.int32)) == np.int32(np.uint32(2166136261 | 1).view(np.int32))
