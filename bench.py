@@ -284,6 +284,21 @@ def bench_gemms(a):
     qkv_fn(); o_fn()
     ms_q, _ = time_fn(qkv_fn, a.steps, a.warmup, not a.no_graph)
     ms_o, _ = time_fn(o_fn, a.steps, a.warmup, not a.no_graph)
+    # this build's own QKV kernel (clef_hip_qkv_gemm) on the same operands, with C1's plan: the
+    # product alone, and with the K/V prologue fused into its epilogue
+    from cleffa_amd import AttnPlan, TextAttention, workloads
+    wl = workloads.config("C1", seed=a.seed)
+    att = TextAttention(24, 4, 256, 64, rope_theta=1e7)
+    plan = AttnPlan(wl["cu_seqlens"], causal=True)
+    qn, kn, p3 = wl["q_norm"].cuda(), wl["k_norm"].cuda(), wl["pos3"].cuda()
+    kp, vt = att.planes(plan.kvT)
+    cs = att.rope_table(T)
+    own_fn = lambda: att.project(xn, wqkv, plan, qkv=qkv, prologue=False)
+    fused_fn = lambda: att.project(xn, wqkv, plan, qn, kn, p3, qkv=qkv, k_plane=kp, vt_plane=vt, rope_cs=cs)
+    own_fn(); fused_fn()
+    ms_own, _ = time_fn(own_fn, a.steps, a.warmup, not a.no_graph)
+    ms_fused, _ = time_fn(fused_fn, a.steps, a.warmup, not a.no_graph)
+    t_own, t_fused = f_qkv / (ms_own * 1e-3) / 1e12, f_qkv / (ms_fused * 1e-3) / 1e12
     tq, to = f_qkv / (ms_q * 1e-3) / 1e12, f_o / (ms_o * 1e-3) / 1e12
     ms = ms_q + ms_o
     print(json.dumps({
@@ -294,6 +309,9 @@ def bench_gemms(a):
         "config": {"workload": "G: QKV 4096x14336x5120 -> bf16, o_proj 4096x5120x6144 += f32"},
         "qkv": {"ms": round(ms_q, 5), "tflops": round(tq, 1), "frac": round(tq / PEAK_BF16_TFLOPS, 4)},
         "o_proj": {"ms": round(ms_o, 5), "tflops": round(to, 1), "frac": round(to / PEAK_BF16_TFLOPS, 4)},
+        "qkv_own_kernel": {"ms": round(ms_own, 5), "tflops": round(t_own, 1), "frac": round(t_own / PEAK_BF16_TFLOPS, 4)},
+        "qkv_own_fused_prologue": {"ms": round(ms_fused, 5), "tflops": round(t_fused, 1),
+                                   "frac": round(t_fused / PEAK_BF16_TFLOPS, 4)},
         "roofline": {"bound": "mfma", "kernel": "hipBLASLt (QKV)", "achieved": round(tq, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tq / PEAK_BF16_TFLOPS, 4), "traffic": None,
                      "launch_ms": round(ms_q, 5)},

@@ -25,7 +25,7 @@ EXPORTS = (
     "clef_hip_rope_inv_freq", "clef_hip_vis_positions", "clef_hip_attn_prep_kv",
     "clef_hip_attn_core", "clef_hip_attn_prefill", "clef_hip_vis_attention", "clef_hip_vis_attention_noalloc",
     "clef_hip_record_positions", "clef_hip_pack_batch",
-    "clef_hip_gemm",
+    "clef_hip_gemm", "clef_hip_qkv_gemm",
     "clef_hip_omni_rope_table", "clef_hip_omni_prep", "clef_hip_omni_plan_max_blocks",
     "clef_hip_omni_plan", "clef_hip_omni_attention",
     "clef_hip_prefix_capacity", "clef_hip_prefix_plane_bytes", "clef_hip_prefix_copy",
@@ -114,6 +114,8 @@ def load():
     lib.clef_hip_gemm.argtypes = [c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_size_t,
                                   c_void_p, c_char_p, c_size_t]
     lib.clef_hip_gemm.restype = c_bool
+    lib.clef_hip_qkv_gemm.argtypes = [c_int, c_void_p, c_void_p, POINTER(AttnArgs), c_void_p, c_void_p, c_char_p, c_size_t]
+    lib.clef_hip_qkv_gemm.restype = c_bool
     lib.clef_hip_omni_rope_table.argtypes = [c_float, POINTER(c_float)]
     lib.clef_hip_omni_rope_table.restype = None
     lib.clef_hip_omni_prep.argtypes = [POINTER(OmniPrepArgs), c_void_p, c_char_p, c_size_t]

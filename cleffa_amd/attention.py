@@ -244,8 +244,9 @@ class TextAttention:
             _check(vt_plane, "vt_plane", (self.nkv, self.hd, kvT), torch.bfloat16, dev)
         if kvT < plan.kv_rows or kvT % 8:
             raise ValueError(f"kvT {kvT} must be >= {plan.kv_rows} and a multiple of 8")
-        _check(out, "out", (T, self.nh * self.hd), {OUT_BF16: torch.bfloat16, OUT_F16: torch.float16,
-                                                    OUT_F32: torch.float32}[out_type], dev)
+        if out is not None:   # None: a call that writes no output (the prologue, the QKV GEMM)
+            _check(out, "out", (T, self.nh * self.hd), {OUT_BF16: torch.bfloat16, OUT_F16: torch.float16,
+                                                        OUT_F32: torch.float32}[out_type], dev)
         if ovf is not None:
             _check(ovf, "ovf", (T,), torch.int32, dev)
         if rope_cs is not None:
@@ -302,6 +303,38 @@ class TextAttention:
         err = _err()
         _lib.check(fn(ctypes.byref(a), _stream_handle(stream), err, len(err)), err)
         return out
+
+
+    def project(self, X, W, plan, q_norm=None, k_norm=None, pos3=None, qkv=None, k_plane=None, vt_plane=None,
+                kvT=None, ovf=None, f16_lim=65504.0, rope_cs=None, prologue=True, stream=None):
+        """The QKV projection qkv = X . W^T (X [T][H] bf16, W [row][H] bf16, the attn_qkv weight as
+        stored) through clef_hip_qkv_gemm. With prologue, its epilogue also writes the K / V^T
+        planes (and rope_cs) as the "prep" stage would, so forward(stage="core") may follow on
+        the same planes and table. Returns qkv."""
+        dev = self.device
+        T, H = plan.T, X.shape[1] if X.dim() == 2 else -1
+        _check(X, "X", (T, H), torch.bfloat16, dev)
+        _check(W, "W", (self.row, H), torch.bfloat16, dev)
+        if qkv is None:
+            qkv = torch.empty((T, self.row), dtype=torch.bfloat16, device=dev)
+        _check(qkv, "qkv", (T, self.row), torch.bfloat16, dev)
+        if prologue:
+            if k_plane is None:
+                kvT = plan.kvT
+                k_plane, vt_plane = self.planes(kvT)
+            elif kvT is None:
+                kvT = k_plane.shape[1]
+            a = self.args(qkv, q_norm, k_norm, pos3, plan, None, k_plane, vt_plane, kvT, ovf=ovf, f16_lim=f16_lim,
+                          rope_cs=rope_cs, schedule=False)
+        else:   # the product alone: only the geometry and the output rows
+            a = AttnArgs()
+            a.nh, a.nkv, a.hd, a.n_rot, a.T, a.row = self.nh, self.nkv, self.hd, self.n_rot, T, self.row
+            a.qkv, a.qkv_type = _ptr(qkv), _lib.QKV_BF16
+        err = _err()
+        _lib.check(_lib.load().clef_hip_qkv_gemm(H, X.data_ptr(), W.data_ptr(), ctypes.byref(a),
+                                                 _ptr(plan.tok_kv) if prologue else None,
+                                                 _stream_handle(stream), err, len(err)), err)
+        return qkv
 
 
 class VisionAttention:

@@ -14,6 +14,7 @@
 #include "attn_text.h"
 #include "attn_text_f32.h"
 #include "attn_vis.h"
+#include "gemm_kernel.h"
 #include "attn_params.h"
 #include "clef_hip_attn.h"
 
@@ -530,6 +531,41 @@ bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, si
     else
         hipLaunchKernelGGL(attn_text_kernel<0>, dim3((unsigned)grid), dim3(512), 0, (hipStream_t)stream, p);
     return launch_ok("attn_fwd<256>", err, errlen);
+}
+
+bool clef_hip_qkv_gemm(int H, const uint16_t *X, const uint16_t *W, const clef_hip_attn_args *a, const int32_t *tok_kv,
+                       void *stream, char *err, size_t errlen) {
+    if (!a) return fail(err, errlen, "null attention arguments");
+    if (a->qkv_type != CLEF_HIP_QKV_BF16) return fail(err, errlen, "the QKV GEMM writes bf16 qkv rows (qkv_type 0)");
+    if (tok_kv ? !check_text(a, false, err, errlen)
+               : (a->hd != 256 || a->nh <= 0 || a->nkv <= 0 || a->nh % a->nkv || a->T < 0 || !a->qkv || !aligned16(a->qkv)))
+        return tok_kv ? false : fail(err, errlen, "bad QKV GEMM geometry or qkv pointer");
+    const long N = 2L * a->nh * a->hd + 2L * a->nkv * a->hd;
+    if (a->row < N || a->row % 8) return fail(err, errlen, "qkv row %d must be >= %ld and a multiple of 8", a->row, N);
+    if (H <= 0 || H % gemm::BK) return fail(err, errlen, "hidden size %d must be a positive multiple of %d", H, gemm::BK);
+    if (!X || !W || !aligned16(X) || !aligned16(W)) return fail(err, errlen, "X and W must be 16-byte aligned device pointers");
+    if ((long)a->T * H * 2 >= (1L << 32) || N * H * 2 >= (1L << 32))
+        return fail(err, errlen, "X or W above 4 GiB (32-bit fill offsets)");
+    if (tok_kv && a->n_rot && a->n_rot != 64) return fail(err, errlen, "the fused prologue takes n_rot 0 or 64 (got %d)", a->n_rot);
+    if (a->T == 0) return true;
+    gemm::Params p;
+    memset(&p, 0, sizeof(p));
+    p.X = X; p.W = W; p.Y = (uint16_t *)a->qkv;
+    p.T = a->T; p.N = (int)N; p.K = H; p.ldy = a->row;
+    p.m_tiles = (a->T + gemm::BM - 1) / gemm::BM;
+    p.n_tiles = (int)(N / gemm::BN);
+    p.n_per_xcd = (p.n_tiles + 7) / 8;
+    if (tok_kv) {
+        p.kv = 1; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
+        p.eps = a->eps; p.f16_lim = f16_limit(a->f16_lim);
+        p.k_norm = a->k_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq; p.tok_kv = tok_kv;
+        p.seq_start = a->seq_start; p.ovf = a->ovf;
+        p.k_plane = (uint16_t *)a->k_plane; p.vt_plane = (uint16_t *)a->vt_plane;
+        p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
+    }
+    const long grid = 8L * p.n_per_xcd * p.m_tiles;
+    hipLaunchKernelGGL(gemm::qkv_gemm_kernel, dim3((unsigned)grid), dim3(gemm::THREADS), 0, (hipStream_t)stream, p);
+    return launch_ok("qkv_gemm", err, errlen);
 }
 
 bool clef_hip_attn_prefill(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {

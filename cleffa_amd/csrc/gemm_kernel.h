@@ -1,0 +1,300 @@
+// The QKV projection on CDNA4 with the text path's K/V prologue in its epilogue: Y = X . W^T
+// (X [T][K] bf16 activations, W [N][K] bf16 weights, both K-contiguous as the model file stores
+// them; f32 accumulation), the role of clef_metal_gemm (clef_metal.m:463-499) at its QKV call
+// (clef_metal.m:1326).
+//
+// Tiles of 128 rows x 256 columns, one per workgroup of 8 waves (2 per SIMD). A 256-column tile
+// of the QKV output is exactly one head's slice (a query or gate half of a q head, one K head or
+// one V head), so the epilogue of a K tile holds whole key rows: it runs the RMSNorm, rotary and
+// f16 split of the K/V prologue on them and writes the K plane rows; a V tile writes its V^T
+// plane entries. Every output tile also leaves its bf16 rows in the qkv buffer.
+//   k loop:   64-deep K slices of X and W stream global -> LDS with global_load_lds (16 bytes a
+//             lane), three stages deep (two slices in flight while one is read), into unpadded
+//             128-byte rows whose 16-byte chunks are XOR-swizzled ((row >> 1) & 7), so the
+//             ds_read_b128 operand reads of 16 consecutive rows hit distinct banks.
+//   products: v_mfma_f32_16x16x32_bf16, each wave a 64 x 64 block of the tile: A = 16 columns
+//             of W (16 output columns), B = 16 rows of X (16 output rows), so a lane's four
+//             accumulators are four consecutive columns of one output row.
+//   epilogue: accumulators rounded to bf16 into an LDS copy of the tile, then coalesced row
+//             stores; K and V tiles take the prologue from that copy, so their planes hold
+//             bitwise what text_prep_kv_kernel makes of the same bf16 rows.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attn_kernels.h"
+
+namespace clef_hip {
+namespace gemm {
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+constexpr int BM = 128, BN = 256, BK = 64, STAGES = 3, THREADS = 512, HD = 256;
+constexpr int A_BYTES = BM * BK * 2;                 // 16 KB
+constexpr int B_BYTES = BN * BK * 2;                 // 32 KB
+constexpr int STAGE_BYTES = A_BYTES + B_BYTES;       // 48 KB
+constexpr int LDS_BYTES = STAGES * STAGE_BYTES;      // 144 KB
+constexpr int CS = 2 * BN + 16;                      // C-tile row stride in LDS (bytes)
+static_assert(BM * CS <= LDS_BYTES, "the C tile reuses the stage buffers");
+// global_load_lds per thread and stage: X 16 and W 32 one-kilobyte instructions over 8 waves
+constexpr int A_FILLS = A_BYTES / 1024 / 8, B_FILLS = B_BYTES / 1024 / 8, FILLS = A_FILLS + B_FILLS;
+
+struct Params {
+    const uint16_t *X, *W;
+    uint16_t *Y;              // [T][ldy] bf16
+    int T, N, K, ldy;
+    int m_tiles, n_tiles, n_per_xcd;
+    // fused K/V prologue (kv != 0): the QKV layout of the text path
+    int kv, nh, nkv, n_rot, kvT;
+    float eps, f16_lim;
+    const float *k_norm;      // [HD] or NULL
+    const int32_t *pos3;      // [T][3]
+    const float *inv_freq;    // [n_rot / 2]
+    const int32_t *tok_kv;    // [T]: plane row of each pass row's key
+    const int32_t *seq_start; // [T] or NULL
+    int32_t *ovf;             // [T] or NULL
+    uint16_t *k_plane;        // [nkv][kvT][HD] f16
+    uint16_t *vt_plane;       // [nkv][HD][kvT] bf16
+    float *rope_cs;           // [T][n_rot / 2][2] or NULL
+};
+
+__device__ __forceinline__ unsigned lds_u32(const void *p) {
+    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+template <int OFF>
+__device__ __forceinline__ bf16x8 rd16(unsigned addr) {
+    bf16x8 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+    return r;
+}
+template <int N>
+__device__ __forceinline__ void wait8(bf16x8 (&r)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(%8)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
+                 "+v"(r[6]), "+v"(r[7]) : "i"(N));
+}
+
+// Output tile of workgroup b: the N tiles are split in runs of n_per_xcd over the 8 XCDs
+// (workgroup b runs on XCD b % 8, each with its own L2), and an XCD walks its run's tiles row of
+// tiles by row of tiles, so the tiles running together share X rows and W columns in its L2.
+__device__ __forceinline__ bool tile_of(const Params &p, int b, int *tm, int *tn) {
+    const int x = b & 7, j = b >> 3;
+    const int n_lo = x * p.n_per_xcd;
+    const int cnt = min(p.n_tiles - n_lo, p.n_per_xcd);
+    if (cnt <= 0 || j >= cnt * p.m_tiles) return false;
+    *tm = j / cnt;
+    *tn = n_lo + j % cnt;
+    return true;
+}
+
+// The K/V prologue of one 128-row tile of a K head (kh) from the bf16 C tile in LDS: the
+// arithmetic of text_prep_kv_kernel (16 lanes per row, 16 dims per lane, the same operation
+// order), on pass rows instead of plane rows.
+__device__ __forceinline__ void k_epilogue(const Params &p, const uint8_t *ct, int m0, int kh) {
+    const int tid = threadIdx.x, rr = tid >> 4, k = tid & 15;
+    const int half_rot = p.n_rot / 2;
+    float wn[16];
+    if (p.k_norm) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 w4 = *(const float4 *)(p.k_norm + 16 * k + 4 * q);
+            wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
+        }
+    }
+    for (int pass = 0; pass < BM / 32; pass++) {
+        const int row = 32 * pass + rr, t = m0 + row;
+        if (t >= p.T) break;   // rows are in order: the rest of this lane's rows are past T too
+        const u32x4 kw0 = *(const u32x4 *)(ct + row * CS + 32 * k), kw1 = *(const u32x4 *)(ct + row * CS + 32 * k + 16);
+        float x[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[2 * j] = bf_lo(kw0[j]);
+            x[2 * j + 1] = bf_hi(kw0[j]);
+            x[8 + 2 * j] = bf_lo(kw1[j]);
+            x[8 + 2 * j + 1] = bf_hi(kw1[j]);
+        }
+        float2 cs[16];
+        if (half_rot && k < 4) {   // lanes 0-3: pairs 16 (k & 1) .. +15 (lanes 2, 3 hold the partners)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int i = 16 * (k & 1) + e;
+                const float ang = (float)p.pos3[3 * (size_t)t + i % 3] * p.inv_freq[i];
+                float sn, cn;
+                rope_sincos(ang, &sn, &cn);
+                cs[e] = make_float2(cn, sn);
+            }
+            if (p.rope_cs && kh == 0 && k < 2) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) *(float2 *)(p.rope_cs + (size_t)t * 2 * half_rot + 2 * (16 * k + e)) = cs[e];
+            }
+        }
+        if (p.k_norm) {
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; e++) ss += x[e] * x[e];
+            ss = row16_sum(ss);
+            const float inv = rsqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+            for (int e = 0; e < 16; e++) x[e] *= inv * wn[e];
+        }
+        if (half_rot) {
+            float y[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const float up = __builtin_amdgcn_update_dpp(0.f, x[e], 0x12e, 0xf, 0xf, false);   // lane + 2
+                const float dn = __builtin_amdgcn_update_dpp(0.f, x[e], 0x122, 0xf, 0xf, false);   // lane - 2
+                y[e] = (k & 2) ? dn : up;
+            }
+            if (k < 4) {
+                const bool first = k < 2;
+#pragma unroll
+                for (int e = 0; e < 16; e++) x[e] = first ? x[e] * cs[e].x - y[e] * cs[e].y : x[e] * cs[e].x + y[e] * cs[e].y;
+            }
+        }
+        bool bad = false;
+        const unsigned lim = __float_as_uint(p.f16_lim);
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const bool over = (__float_as_uint(x[e]) & 0x7fffffffu) > lim;
+            x[e] = over ? copysignf(65504.f, x[e]) : x[e];
+            bad |= over;
+        }
+        if (bad && p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint16_t *dst = p.k_plane + ((size_t)kh * p.kvT + p.tok_kv[t]) * HD + 16 * k;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const float *xs = x + 8 * h;
+            u32x4 ko = {pack_f16(xs[0], xs[1]), pack_f16(xs[2], xs[3]), pack_f16(xs[4], xs[5]), pack_f16(xs[6], xs[7])};
+            *(u32x4 *)(dst + 8 * h) = ko;
+        }
+    }
+}
+
+// V^T entries of one tile of a V head (kh): lane = pass row, so each store of a dim covers 64
+// consecutive plane rows of a record (2 bytes a lane). Only the pass's own plane rows are
+// written. Values with |v| > f16_lim or NaN saturate to +-65536 and flag the record, as in
+// text_prep_kv_kernel.
+__device__ __forceinline__ void v_epilogue(const Params &p, const uint8_t *ct, int m0, int kh) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int row = 64 * (wave & 1) + lane, t = m0 + row, d0 = 64 * (wave >> 1);
+    if (t >= p.T) return;
+    const size_t prow = (size_t)p.tok_kv[t];
+    uint16_t *col = p.vt_plane + ((size_t)kh * HD + d0) * p.kvT + prow;
+    bool bad = false;
+#pragma unroll 8
+    for (int d = 0; d < 64; d += 2) {
+        unsigned w = *(const unsigned *)(ct + row * CS + 2 * (d0 + d));
+        const bool lo_bad = !(__uint_as_float((w & 0x7fffu) << 16) <= p.f16_lim),
+                   hi_bad = !(__uint_as_float(w & 0x7fff0000u) <= p.f16_lim);
+        if (lo_bad) w = (w & 0xffff8000u) | 0x4780u;
+        if (hi_bad) w = (w & 0x8000ffffu) | 0x47800000u;
+        bad |= lo_bad | hi_bad;
+        col[(size_t)d * p.kvT] = (uint16_t)w;
+        col[(size_t)(d + 1) * p.kvT] = (uint16_t)(w >> 16);
+    }
+    if (bad && p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(THREADS, 1) void qkv_gemm_kernel(Params p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+    int tm, tn;
+    if (!tile_of(p, blockIdx.x, &tm, &tn)) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    // Fill offsets (bytes from the slice's first element): instruction j of a tile covers LDS
+    // rows 8j .. 8j + 7; lane l lands in row 8j + l / 8 at chunk position l % 8, which holds the
+    // row's k-chunk (l % 8) ^ ((row >> 1) & 7).
+    unsigned fo[FILLS];
+#pragma unroll
+    for (int f = 0; f < FILLS; f++) {
+        const bool a = f < A_FILLS;
+        const int j = a ? wave * A_FILLS + f : wave * B_FILLS + (f - A_FILLS);
+        const int row = 8 * j + (lane >> 3);
+        const int c = (lane & 7) ^ ((row >> 1) & 7);
+        const int grow = a ? min(m0 + row, p.T - 1) : n0 + row;
+        fo[f] = ((unsigned)grow * (unsigned)p.K + (unsigned)(8 * c)) * 2u;
+    }
+    auto fill = [&](int slice, int stage) {
+        const char *xa = (const char *)(p.X + (size_t)slice * BK), *wa = (const char *)(p.W + (size_t)slice * BK);
+        uint8_t *sa = lds + stage * STAGE_BYTES;
+#pragma unroll
+        for (int f = 0; f < FILLS; f++) {
+            const bool a = f < A_FILLS;
+            const int j = a ? wave * A_FILLS + f : wave * B_FILLS + (f - A_FILLS);
+            unsigned off = fo[f];
+            asm volatile("" : "+v"(off));
+            uint8_t *dst = a ? sa + 1024 * j : sa + A_BYTES + 1024 * j;
+            __builtin_amdgcn_global_load_lds((const void *)((a ? xa : wa) + off), (lds_void *)dst, 16, 0, 0);
+        }
+    };
+    // operand read addresses: rows (lane & 15) of the wave's 64-row blocks, k-chunk 4 ks + lane / 16
+    const int wm = wave >> 2, wn = wave & 3, r16 = lane & 15, g = lane >> 4, sw = (r16 >> 1) & 7;
+    const unsigned base = lds_u32(lds);
+    unsigned xa[2], wa[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+        const unsigned ch = (unsigned)(((4 * ks + g) ^ sw) * 16);
+        xa[ks] = base + (unsigned)((64 * wm + r16) * 128) + ch;
+        wa[ks] = base + A_BYTES + (unsigned)((64 * wn + r16) * 128) + ch;
+    }
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int nk = p.K / BK;
+    fill(0, 0);
+    if (nk > 1) fill(1, 1);
+    int stage = 0;
+    for (int it = 0; it < nk; it++) {
+        // this wave's fills of slice it have landed (those of it + 1 may still be in flight), and
+        // every wave has left slice it - 1, whose buffer the fills of it + 2 take
+        if (it + 1 < nk) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(FILLS) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (it + 2 < nk) fill(it + 2, stage == 0 ? 2 : stage - 1);
+        const unsigned so = (unsigned)(stage * STAGE_BYTES);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            bf16x8 r[8];   // W columns 0-3, X rows 0-3 of the wave's block
+            const unsigned wk = wa[ks] + so, xk = xa[ks] + so;
+            r[0] = rd16<0>(wk); r[1] = rd16<2048>(wk); r[2] = rd16<4096>(wk); r[3] = rd16<6144>(wk);
+            r[4] = rd16<0>(xk); r[5] = rd16<2048>(xk); r[6] = rd16<4096>(xk); r[7] = rd16<6144>(xk);
+            wait8<0>(r);
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r[nt], r[4 + mt], acc[mt][nt], 0, 0, 0);
+        }
+        stage = stage == STAGES - 1 ? 0 : stage + 1;
+    }
+
+    // ---- epilogue: bf16 C tile into LDS (every wave has left the stage buffers)
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) {
+            const int row = 64 * wm + 16 * mt + r16, c = 64 * wn + 16 * nt + 4 * g;
+            const f32x4 v = acc[mt][nt];
+            *(u32x2 *)(lds + row * CS + 2 * c) = u32x2{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])};
+        }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < BM * BN * 2 / 16 / THREADS; i++) {
+        const int id = tid + THREADS * i, row = id >> 5, c16 = id & 31;
+        if (m0 + row < p.T)
+            *(u32x4 *)(p.Y + (size_t)(m0 + row) * p.ldy + n0 + 8 * c16) = *(const u32x4 *)(lds + row * CS + 16 * c16);
+    }
+    if (p.kv) {
+        const int kcol = 2 * p.nh * HD;
+        if (n0 >= kcol && n0 < kcol + p.nkv * HD) k_epilogue(p, lds, m0, (n0 - kcol) / HD);
+        else if (n0 >= kcol + p.nkv * HD) v_epilogue(p, lds, m0, (n0 - kcol - p.nkv * HD) / HD);
+    }
+}
+
+}  // namespace gemm
+}  // namespace clef_hip

@@ -175,6 +175,18 @@ int clef_hip_attn_sched_size(int n_blk, int nh, int n_wg);
 bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, int n_wg,
                             int32_t *sched, int max_sched, char *err, size_t errlen);
 
+/* The QKV projection with the K/V prologue fused into its epilogue: qkv[T][row] (bf16, a->qkv)
+ * = X . W^T with X [T][H] bf16 activations and W [N][H] the attn_qkv weight as stored
+ * (N = 2 nh hd + 2 nkv hd columns: [q | gate] per q head, then K heads, then V heads), f32
+ * accumulation; replaces clef_metal_gemm at the QKV call (clef_metal.m:463-499, 1326) and the
+ * attn_prep K/V kernels (metal/clef.metal:245-300, 873-928). tok_kv (the plan's pass row ->
+ * plane row map, [T]) != NULL: every K head's rows are normalised, rotated and written to the K
+ * plane and every V head's to the V^T plane, bitwise what clef_hip_attn_prep_kv writes from the
+ * same qkv rows (with the same flags and rope_cs), so clef_hip_attn_core may follow directly;
+ * NULL: the product only. H must be a multiple of 64; X and W at most 4 GiB each. */
+bool clef_hip_qkv_gemm(int H, const uint16_t *X, const uint16_t *W, const clef_hip_attn_args *a, const int32_t *tok_kv,
+                       void *stream, char *err, size_t errlen);
+
 /* K/V prologue only: RMSNorm + rotary of each pass row's K into its plane row (kv_tok), V into
  * the V^T plane (attn_prep / attn_prep_split / attn_prep_prefix K and V parts,
  * metal/clef.metal:245-300, 657-707, 873-928). Plane rows with kv_tok -1 are not written. */
