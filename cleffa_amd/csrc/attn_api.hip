@@ -542,7 +542,7 @@ bool clef_hip_qkv_gemm(int H, const uint16_t *X, const uint16_t *W, const clef_h
         return tok_kv ? false : fail(err, errlen, "bad QKV GEMM geometry or qkv pointer");
     const long N = 2L * a->nh * a->hd + 2L * a->nkv * a->hd;
     if (a->row < N || a->row % 8) return fail(err, errlen, "qkv row %d must be >= %ld and a multiple of 8", a->row, N);
-    if (H <= 0 || H % gemm::BK) return fail(err, errlen, "hidden size %d must be a positive multiple of %d", H, gemm::BK);
+    if (H <= 0 || H % gemm::KALIGN) return fail(err, errlen, "hidden size %d must be a positive multiple of %d", H, gemm::KALIGN);
     if (!X || !W || !aligned16(X) || !aligned16(W)) return fail(err, errlen, "X and W must be 16-byte aligned device pointers");
     if ((long)a->T * H * 2 >= (1L << 32) || N * H * 2 >= (1L << 32))
         return fail(err, errlen, "X or W above 4 GiB (32-bit fill offsets)");
@@ -552,7 +552,6 @@ bool clef_hip_qkv_gemm(int H, const uint16_t *X, const uint16_t *W, const clef_h
     memset(&p, 0, sizeof(p));
     p.X = X; p.W = W; p.Y = (uint16_t *)a->qkv;
     p.T = a->T; p.N = (int)N; p.K = H; p.ldy = a->row;
-    p.m_tiles = (a->T + gemm::BM - 1) / gemm::BM;
     p.n_tiles = (int)(N / gemm::BN);
     p.n_per_xcd = (p.n_tiles + 7) / 8;
     if (tok_kv) {
@@ -563,8 +562,14 @@ bool clef_hip_qkv_gemm(int H, const uint16_t *X, const uint16_t *W, const clef_h
         p.k_plane = (uint16_t *)a->k_plane; p.vt_plane = (uint16_t *)a->vt_plane;
         p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
     }
+    // 256 x 256 tiles, 8 waves of 128 x 64, 64-deep K slices double-buffered (128 KB of LDS):
+    // 128-row tiles moved 1.5x the operand bytes per product and ran fill-bound (0.59 against
+    // 0.53 ms at 4096 x 14336 x 5120); 32-deep slices four deep and 64 x 128 wave blocks measured
+    // no better
+    using C = gemm::Cfg<256, 128, 64, 64, 2>;
+    p.m_tiles = (a->T + C::BM - 1) / C::BM;
     const long grid = 8L * p.n_per_xcd * p.m_tiles;
-    hipLaunchKernelGGL(gemm::qkv_gemm_kernel, dim3((unsigned)grid), dim3(gemm::THREADS), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(gemm::qkv_gemm_kernel<C>, dim3((unsigned)grid), dim3(C::THREADS), 0, (hipStream_t)stream, p);
     return launch_ok("qkv_gemm", err, errlen);
 }
 
