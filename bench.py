@@ -1,14 +1,17 @@
 """Benchmark of the prefill attention hot path on one MI355X.
 
-One step = one full-attention layer over the C1 micro-batch (8 packed causal records, 4,096
-tokens, 24/4 heads, hd 256): the K/V prologue kernel plus the attention kernel with the fused
-Q prologue and gate epilogue, on inputs already resident in HBM. Steps are replayed from a HIP
-graph (captured once) so host launch cost is not part of the GPU time; the timed region is
-bracketed by torch.cuda.synchronize() and HIP events on the launch stream.
+One step = one full-attention layer's attention over the C1 micro-batch (8 packed causal
+records, 4,096 tokens, 24/4 heads, hd 256): the K/V prologue kernel plus the attention kernel
+with the fused Q prologue and gate epilogue, on qkv rows already resident in HBM. Steps are
+replayed from a HIP graph (captured once) so host launch cost is not part of the GPU time; the
+timed region is bracketed by torch.cuda.synchronize() and HIP events on the launch stream.
 
 Prints one JSON line. `value` is algorithmic TFLOP/s of the whole step (QK^T + PV flops,
-4*hd*nh*pairs); `roofline` covers the attention kernel alone, timed the same way;
-`cpu_baseline` is the fp32 CPU oracle (OpenMP) on the same C1 inputs.
+4*hd*nh*pairs); `roofline` covers the attention kernel alone, priced at its time inside the
+step (the step minus the prologue kernel timed alone, `launch_ms_in_step`), with its time in
+back-to-back replays beside it (`launch_ms`); `layer` times the engine's layer instead: the
+QKV GEMM whose epilogue writes the K / V^T planes (no prologue kernel), then the attention
+kernel; `cpu_baseline` is the fp32 CPU oracle (OpenMP) on the same C1 inputs.
 """
 import argparse
 import json
@@ -58,6 +61,8 @@ def parse():
                          "FP32 kernels); the roofline is then priced against the fp32 MFMA peak")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
+    ap.add_argument("--no-layer", action="store_true",
+                    help="skip the layer diagnostics (QKV GEMM with the fused K/V prologue, then the attention kernel)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="for rocprofv3 --pmc: a 256 MiB device copy and a 256 MiB elementwise pass "
                          "(counter calibration), then 3 eager "
@@ -83,7 +88,7 @@ def build_step(cfg, seed, fp32=False):
         info = dict(workload="C4 vision: 4 images x 1,024 patches (32x32), bidirectional, 16 heads MHA, "
                     "hd 72, 2-D rotary", tokens=plan.T, pairs=plan.pairs(), hd=w["hd"], nh=w["heads"],
                     bytes=plan.T * 3 * vis.E * 2 + plan.T * vis.E * 2, core=None)
-        return step, None, info, w
+        return step, None, None, info, w
     att = TextAttention(w["nh"], w["nkv"], w["hd"], w["n_rot"], rope_theta=w["theta"], device=dev)
     if cfg == "C3":
         plan = AttnPlan(w["cu_seqlens"], w["cu_seqlens_k"], causal=True, device=dev)
@@ -103,6 +108,19 @@ def build_step(cfg, seed, fp32=False):
     args = (w["qkv"], w["q_norm"], w["k_norm"], w["pos3"], plan)
     step = lambda: att.forward(*args, stage="prefill", **kwargs)
     core = lambda: att.forward(*args, stage="core", **kwargs)
+    prep = lambda: att.forward(*args, stage="prep", **kwargs)
+    layer = None
+    if not fp32:
+        # The engine's path: the QKV GEMM (hidden 5,120, the 27B width) writes the qkv rows and,
+        # in its epilogue, the K / V^T planes and rope_cs; the attention kernel follows.
+        X, Wq = workloads.qkv_projection(plan.T, w["nh"], w["nkv"], w["hd"], H=5120, seed=seed, device=dev,
+                                         outlier_frac=0.0 if cfg in ("C0", "C2", "C3") else 0.02)
+        qkv_out = torch.empty_like(w["qkv"])
+        fused = lambda: att.project(X, Wq, plan, w["q_norm"], w["k_norm"], w["pos3"], qkv=qkv_out, k_plane=kp,
+                                    vt_plane=vt, kvT=kvT, rope_cs=kwargs["rope_cs"])
+        plain = lambda: att.project(X, Wq, plan, qkv=qkv_out, prologue=False)
+        core_l = lambda: att.forward(qkv_out, w["q_norm"], w["k_norm"], w["pos3"], plan, stage="core", **kwargs)
+        layer = dict(fused=fused, plain=plain, layer=lambda: (fused(), core_l()), H=5120)
     T, nh, nkv, hd = plan.T, w["nh"], w["nkv"], w["hd"]
     # algorithmic bytes: qkv rows read once, O written once, cached K/V read (C3)
     esz = 4 if fp32 else 2
@@ -122,8 +140,8 @@ def build_step(cfg, seed, fp32=False):
     kv_rows = int(w["cu_seqlens_k"][-1]) if cfg == "C3" else T
     core_bytes = T * 2 * nh * hd * esz + 2 * nkv * kv_rows * hd * (4 if fp32 else 2) + T * nh * hd * 2
     info = dict(workload=names[cfg], tokens=T, pairs=plan.pairs(), hd=hd, nh=nh, bytes=nbytes, core_bytes=core_bytes,
-                lengths=[int(x) for x in np.diff(plan.cu_q)])
-    return step, core, info, w
+                lengths=[int(x) for x in np.diff(plan.cu_q)], layer=layer)
+    return step, core, prep, info, w
 
 
 def time_fn(fn, steps, warmup, graph):
@@ -367,7 +385,7 @@ def main():
         return bench_gemms(a)
     if a.config == "M":
         return bench_mfma_ceiling(a)
-    step, core, info, w = build_step(a.config, a.seed, a.fp32)
+    step, core, prep, info, w = build_step(a.config, a.seed, a.fp32)
     if a.profile_pass:
         src = torch.randn(CALIB_BYTES // 2, device="cuda").to(torch.bfloat16)
         dst = torch.empty_like(src)
@@ -381,6 +399,22 @@ def main():
         return
     graph = not a.no_graph
     ms, wall_ms = time_fn(step, a.steps, a.warmup, graph)
+    layer = info.get("layer")
+    layer_info = None
+    if layer is not None and not a.no_layer:
+        # The engine's layer: the QKV GEMM with the K/V prologue in its epilogue, then the
+        # attention kernel. Medians of interleaved runs; the attention's share of the layer is
+        # (GEMM with prologue + kernel) - plain GEMM.
+        t = {"layer": [], "plain": [], "fused": []}
+        for _ in range(3):
+            for k in t:
+                t[k].append(time_fn(layer[k], a.steps, a.warmup, graph)[0])
+        med = {k: statistics.median(v) for k, v in t.items()}
+        layer_info = {"hidden": layer["H"], "layer_ms": round(med["layer"], 5), "qkv_gemm_ms": round(med["plain"], 5),
+                      "qkv_gemm_fused_prologue_ms": round(med["fused"], 5),
+                      "prologue_in_gemm_ms": round(med["fused"] - med["plain"], 5),
+                      "attention_share_of_layer_ms": round(med["layer"] - med["plain"], 5),
+                      "core_in_layer_ms": round(med["layer"] - med["fused"], 5)}
     flops = 4.0 * info["hd"] * info["nh"] * info["pairs"]
     tflops = flops / (ms * 1e-3) / 1e12
     res = {
@@ -417,7 +451,18 @@ def main():
             ceil_tf, ceil_ghz = mfma_ceiling(True)
             res["roofline"].update({"mfma_stream_ceiling": round(ceil_tf, 1), "mfma_stream_clock_ghz": round(ceil_ghz, 3),
                                     "frac_of_stream_ceiling": round(achieved / ceil_tf, 4)})
-        res["prep_ms"] = round(ms - core_ms, 5)
+        # the kernel as it runs inside the step: the step minus the K/V prologue kernel alone
+        prep_ms, _ = time_fn(prep, a.steps, a.warmup, graph)
+        in_step = ms - prep_ms
+        ach = flops / (in_step * 1e-3) / 1e12
+        res["roofline"].update({"launch_ms_in_step": round(in_step, 5), "achieved_replay": res["roofline"]["achieved"],
+                                "frac_replay": res["roofline"]["frac"], "achieved": round(ach, 2),
+                                "frac": round(ach / peak, 4)})
+        if "frac_of_stream_ceiling" in res["roofline"]:
+            res["roofline"]["frac_of_stream_ceiling"] = round(ach / res["roofline"]["mfma_stream_ceiling"], 4)
+        res["prep_ms"] = round(prep_ms, 5)
+        if layer_info is not None:
+            res["layer"] = layer_info
     if not a.no_cpu and a.config == "C1" and not a.fp32:
         sec, threads = cpu_baseline(w, a.config)
         res["cpu_baseline"] = {"value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s",

@@ -40,7 +40,7 @@ struct Params {
     const uint16_t *X, *W;
     uint16_t *Y;              // [T][ldy] bf16
     int T, N, K, ldy;
-    int m_tiles, n_tiles, n_per_xcd;
+    int m_tiles, n_tiles, n_per_xcd;   // n_per_xcd: the most N tiles any XCD owns
     // fused K/V prologue (kv != 0): the QKV layout of the text path
     int kv, nh, nkv, n_rot, kvT;
     float eps, f16_lim;
@@ -73,16 +73,16 @@ __device__ __forceinline__ void static_for_g(F &&f) {
     static_for_g_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// Output tile of workgroup b: the N tiles are split in runs of n_per_xcd over the 8 XCDs
-// (workgroup b runs on XCD b % 8, each with its own L2), and an XCD walks its run's tiles row of
-// tiles by row of tiles, so the tiles running together share X rows and W columns in its L2.
+// Output tile of workgroup b: XCD x (workgroup b runs on XCD b % 8, each with its own L2) owns
+// the N tiles x, x + 8, x + 16, ... and walks them row of tiles by row of tiles, so the tiles
+// running together on an XCD share X rows and W columns in its L2. The stride spreads the K and
+// V head tiles (the last 2 nkv N tiles), whose epilogues carry the K/V prologue, over the XCDs.
 __device__ __forceinline__ bool tile_of(const Params &p, int b, int *tm, int *tn) {
     const int x = b & 7, j = b >> 3;
-    const int n_lo = x * p.n_per_xcd;
-    const int cnt = min(p.n_tiles - n_lo, p.n_per_xcd);
+    const int cnt = (p.n_tiles - x + 7) >> 3;
     if (cnt <= 0 || j >= cnt * p.m_tiles) return false;
     *tm = j / cnt;
-    *tn = n_lo + j % cnt;
+    *tn = x + 8 * (j % cnt);
     return true;
 }
 

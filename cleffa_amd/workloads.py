@@ -45,6 +45,32 @@ def _gen(device, seed):
     return g
 
 
+def column_scales(nh, nkv, hd, seed, outlier_frac=0.02, outlier_scale=8.0):
+    """Per-column scale of the qkv rows: 1, or outlier_scale on a random outlier_frac of the query
+    and key channels."""
+    row = 2 * nh * hd + 2 * nkv * hd
+    rng = np.random.default_rng(seed + 7)
+    cols = np.zeros(row, dtype=np.float32) + 1.0
+    qcols = (np.arange(nh)[:, None] * 2 * hd + np.arange(hd)[None, :]).ravel()
+    kcols = 2 * nh * hd + np.arange(nkv * hd)
+    for c in (qcols, kcols):
+        pick = rng.random(c.size) < outlier_frac
+        cols[c[pick]] = outlier_scale
+    return cols
+
+
+def qkv_projection(T, nh, nkv, hd=256, H=5120, seed=0, device="cpu", outlier_frac=0.02, outlier_scale=8.0):
+    """Operands of the QKV GEMM whose product has the distribution text_inputs gives the qkv rows
+    directly: X [T][H] ~ N(0, 1) and W [row][H] ~ N(0, 1 / H) (so each product entry is about
+    N(0, 1)), with the same outlier channels scaled. Both bf16."""
+    g = _gen(device, seed + 101)
+    X = torch.randn((T, H), generator=g, device=device, dtype=torch.float32).to(torch.bfloat16)
+    W = torch.randn((2 * nh * hd + 2 * nkv * hd, H), generator=g, device=device, dtype=torch.float32) * H ** -0.5
+    if outlier_frac > 0:
+        W *= torch.from_numpy(column_scales(nh, nkv, hd, seed, outlier_frac, outlier_scale)).to(device)[:, None]
+    return X, W.to(torch.bfloat16)
+
+
 def text_inputs(lengths, nh, nkv, hd=256, n_rot=64, seed=0, device="cpu", norm=True,
                 outlier_frac=0.02, outlier_scale=8.0, positions=None):
     """Fused qkv rows [T][2*nh*hd + 2*nkv*hd] (bf16), norm weights, pos3 and cu_seqlens.
@@ -54,14 +80,7 @@ def text_inputs(lengths, nh, nkv, hd=256, n_rot=64, seed=0, device="cpu", norm=T
     g = _gen(device, seed)
     qkv = torch.randn((T, row), generator=g, device=device, dtype=torch.float32)
     if outlier_frac > 0:
-        rng = np.random.default_rng(seed + 7)
-        cols = np.zeros(row, dtype=np.float32) + 1.0
-        qcols = (np.arange(nh)[:, None] * 2 * hd + np.arange(hd)[None, :]).ravel()
-        kcols = 2 * nh * hd + np.arange(nkv * hd)
-        for c in (qcols, kcols):
-            pick = rng.random(c.size) < outlier_frac
-            cols[c[pick]] = outlier_scale
-        qkv *= torch.from_numpy(cols).to(device)
+        qkv *= torch.from_numpy(column_scales(nh, nkv, hd, seed, outlier_frac, outlier_scale)).to(device)
     qkv = qkv.to(torch.bfloat16)
     q_norm = k_norm = None
     if norm:

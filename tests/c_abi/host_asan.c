@@ -65,8 +65,12 @@ static void plan_case(const int32_t *cu_q, const int32_t *cu_k, int n_seq, int c
         ok = clef_hip_attn_schedule(blocks, n_blk, nh, nkv, n_wg, sched, sz, err, sizeof err);
         EXPECT(ok, "schedule: %s", err);
         /* every (block, head) covered once by the items' rows (codes 0-3) */
-        const int32_t *offs = sched + 4;
-        EXPECT(offs[0] == 0 && offs[n_wg] <= sz - 4 - n_wg - 1, "sched offsets");
+        /* header {magic, n_blk, nh, n_wg, nkv, fingerprint of the block list (word 7 of every
+           block entry), 0, 0}, then the offsets */
+        EXPECT(sched[0] == 0x53434844 && sched[1] == n_blk && sched[2] == nh && sched[3] == n_wg && sched[4] == nkv &&
+               sched[5] == blocks[7] && sched[5] != 0, "sched header");
+        const int32_t *offs = sched + 8;
+        EXPECT(offs[0] == 0 && offs[n_wg] <= sz - 8 - n_wg - 1, "sched offsets");
         free(sched);
         int32_t *tiny = imalloc(4);
         EXPECT(!clef_hip_attn_schedule(blocks, n_blk, nh, nkv, n_wg, tiny, 4, err, sizeof err), "tiny schedule accepted");
