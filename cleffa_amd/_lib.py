@@ -60,7 +60,7 @@ class AttnArgs(ctypes.Structure):
         ("kv_rows", c_int), ("causal", c_int), ("gate", c_int),
         ("out", c_void_p), ("out_type", c_int), ("f16_lim", c_float), ("ovf", c_void_p),
         ("trace", c_void_p), ("sched", c_void_p), ("n_wg", c_int),
-        ("seq_start", c_void_p), ("qkv_type", c_int),
+        ("seq_start", c_void_p), ("qkv_type", c_int), ("tok_kv", c_void_p),
     ]
 
 

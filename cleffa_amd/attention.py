@@ -270,6 +270,7 @@ class TextAttention:
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
         a.trace = _ptr(trace)
         a.seq_start, a.qkv_type = _ptr(plan.seq_start), _lib.QKV_F32 if fp32 else _lib.QKV_BF16
+        a.tok_kv = _ptr(plan.tok_kv)
         if schedule and plan.n_blk and not fp32:
             # True: one workgroup per CU; an int: that many workgroups
             n_wg = _device_cus(dev) if schedule is True else int(schedule)

@@ -15,6 +15,7 @@
 #include "attn_text_f32.h"
 #include "attn_vis.h"
 #include "gemm_kernel.h"
+#include "kv_rows.h"
 #include "attn_params.h"
 #include "clef_hip_attn.h"
 
@@ -213,6 +214,19 @@ bool core_f32(const clef_hip_attn_args *a, void *stream, char *err, size_t errle
 
 // a pass with fewer (block, head) items than workgroups splits its blocks of more than 64 rows
 bool sched_splits(int n_blk, int nh, int n_wg) { return (long)n_blk * nh < n_wg; }
+
+// The K/V prologue's arguments (kv_rows.h) from the call's: the shared fields of the separate
+// prologue kernel and of the QKV GEMM's epilogue.
+KvRows kv_rows_params(const clef_hip_attn_args *a, const int32_t *tok_kv) {
+    KvRows r;
+    r.T = a->T; r.nh = a->nh; r.nkv = a->nkv; r.n_rot = a->n_rot; r.kvT = a->kvT;
+    r.eps = a->eps; r.f16_lim = f16_limit(a->f16_lim);
+    r.k_norm = a->k_norm; r.pos3 = a->pos3; r.inv_freq = a->inv_freq; r.tok_kv = tok_kv;
+    r.seq_start = a->seq_start; r.ovf = a->ovf;
+    r.k_plane = (uint16_t *)a->k_plane; r.vt_plane = (uint16_t *)a->vt_plane;
+    r.rope_cs = a->n_rot ? a->rope_cs : nullptr;
+    return r;
+}
 
 }  // namespace
 
@@ -485,15 +499,11 @@ bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err,
         hipLaunchKernelGGL(text32::text_prep_kv_f32_kernel, dim3((unsigned)((groups + 7) / 8)), dim3(256), 0, (hipStream_t)stream, p);
         return launch_ok("text_prep_kv_f32", err, errlen);
     }
-    PrepParams p;
-    p.qkv = (const uint16_t *)a->qkv; p.k_norm = a->k_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq;
-    p.kv_tok = a->kv_tok; p.k_plane = (uint16_t *)a->k_plane; p.vt_plane = (uint16_t *)a->vt_plane;
-    p.kv_rows = a->kv_rows; p.row = a->row; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
-    p.eps = a->eps; p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
-    p.seq_start = a->seq_start; p.ovf = a->ovf; p.f16_lim = f16_limit(a->f16_lim);
-    dim3 grid((a->kv_rows + kPrepRows - 1) / kPrepRows, a->nkv);
-    hipLaunchKernelGGL(text_prep_kv_kernel, grid, dim3(16 * kPrepRows), 0, (hipStream_t)stream, p);
-    return launch_ok("text_prep_kv", err, errlen);
+    if (!a->tok_kv) return fail(err, errlen, "the K/V prologue needs tok_kv (the plan's pass row -> plane row map)");
+    dim3 grid((a->T + kPrepRowsBM - 1) / kPrepRowsBM, 2 * a->nkv);
+    hipLaunchKernelGGL(text_prep_rows_kernel, grid, dim3(kPrepRowsThreads), 0, (hipStream_t)stream, (const uint16_t *)a->qkv,
+                       a->row, kv_rows_params(a, a->tok_kv));
+    return launch_ok("text_prep_rows", err, errlen);
 }
 
 bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {
@@ -554,13 +564,10 @@ bool clef_hip_qkv_gemm(int H, const uint16_t *X, const uint16_t *W, const clef_h
     p.T = a->T; p.N = (int)N; p.K = H; p.ldy = a->row;
     p.n_tiles = (int)(N / gemm::BN);
     p.n_per_xcd = (p.n_tiles + 7) / 8;
+    p.r.T = a->T; p.r.nh = a->nh; p.r.nkv = a->nkv;
     if (tok_kv) {
-        p.kv = 1; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot; p.kvT = a->kvT;
-        p.eps = a->eps; p.f16_lim = f16_limit(a->f16_lim);
-        p.k_norm = a->k_norm; p.pos3 = a->pos3; p.inv_freq = a->inv_freq; p.tok_kv = tok_kv;
-        p.seq_start = a->seq_start; p.ovf = a->ovf;
-        p.k_plane = (uint16_t *)a->k_plane; p.vt_plane = (uint16_t *)a->vt_plane;
-        p.rope_cs = a->n_rot ? a->rope_cs : nullptr;
+        p.kv = 1;
+        p.r = kv_rows_params(a, tok_kv);
     }
     // 256 x 256 tiles, 8 waves of 128 x 64, 64-deep K slices double-buffered (128 KB of LDS):
     // 128-row tiles moved 1.5x the operand bytes per product and ran fill-bound (0.59 against

@@ -133,9 +133,7 @@ __device__ __forceinline__ void store_out4(void *out, size_t idx, f32x4_t v, int
 typedef __attribute__((address_space(3))) void lds_void;
 
 // ------------------------------------------------------------------------------------------
-// Text K/V prologue (metal/clef.metal:245-300 and 873-928 for K and V): K = RMSNorm(k) * (1+w)
-// then partial rotary into the f16 K plane [nkv][kvT][HD]; V unnormalised into the V^T plane
-// [nkv][HD][kvT]; the rotary cos/sin of each pass row into rope_cs for the Q prologue.
+// Text K/V prologue helpers (the kernel and its epilogue form live in kv_rows.h).
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ float row16_sum(float v) {   // sum over the lane's 16-lane row
     v += __builtin_amdgcn_update_dpp(0.f, v, 0x128, 0xf, 0xf, false);   // row_ror:8
@@ -143,190 +141,6 @@ __device__ __forceinline__ float row16_sum(float v) {   // sum over the lane's 1
     v += __builtin_amdgcn_update_dpp(0.f, v, 0x4e, 0xf, 0xf, false);    // quad_perm [2,3,0,1]
     v += __builtin_amdgcn_update_dpp(0.f, v, 0xb1, 0xf, 0xf, false);    // quad_perm [1,0,3,2]
     return v;
-}
-
-// K/V prologue over plane rows: workgroup (b, kh) owns plane rows 16b .. 16b+15 of kv head kh
-// and takes each row's key from pass row kv_tok[row] (-1: the row is left as it is). 16 lanes
-// per row, 16 dims per lane. K rows are normalised, rotated and stored whole (512 B per row).
-// V rows are staged row-major in LDS and read back transposed with ds_read_b64_tr_b16 (lane i
-// of a 16-lane group receives element i % 4 of the 8 bytes lane 4j + i / 4 addressed, for
-// j = 0..3), which hands each lane one head dim of 4 consecutive rows; two such reads make a
-// 16-byte V^T run of 8 plane rows. A run with rows the pass does not own (a prefix record's
-// cached rows, rows past a record) is merged with the plane's contents.
-constexpr int kPrepRows = 16;
-typedef short short4_t __attribute__((ext_vector_type(4)));
-__global__ __launch_bounds__(16 * kPrepRows) void text_prep_kv_kernel(PrepParams p) {
-    constexpr int HD = 256, ROWS = kPrepRows, NT = 16 * ROWS;
-    constexpr int VS = HD + 64;   // LDS row stride: 4 rows' 128-byte reads fall in distinct banks
-    __shared__ __attribute__((aligned(16))) uint16_t vl[ROWS * VS];
-    __shared__ __attribute__((aligned(16))) float2 csl[ROWS][32];
-    __shared__ int trow[ROWS];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int rr = tid >> 4, k = tid & 15;       // row of the tile, 16-dim group of the row
-    const int r0 = blockIdx.x * ROWS, kh = blockIdx.y;
-    const int half_rot = p.n_rot / 2;            // 0 or 32: dims [0, 32) pair with [32, 64)
-    const int t = (r0 + rr < p.kv_rows) ? p.kv_tok[r0 + rr] : -1;
-    if (k == 0) trow[rr] = t;
-    if (!__syncthreads_or(t >= 0)) return;       // no row of this tile belongs to the pass
-    // Global loads first, all in flight together: the row's K and V chunks, the positions and
-    // frequencies of this thread's rotary-table entries, the k_norm weights. The loads are
-    // unconditional (a row the pass does not own reads pass row 0) and the values selected after:
-    // a load under a condition becomes a branch, and the compiler waits for it at the join.
-    const uint16_t *src = p.qkv + (size_t)(t >= 0 ? t : 0) * p.row + (size_t)p.nh * 2 * HD + (size_t)kh * HD + 16 * k;
-    u32x4 kw[2], vw[2];
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        kw[h] = *(const u32x4 *)(src + 8 * h);
-        vw[h] = *(const u32x4 *)(src + (size_t)p.nkv * HD + 8 * h);
-    }
-    // rotary table of the tile: ROWS x 32 pairs, pair i turns by axis i % 3; entry idx = tid + NT j
-    constexpr int TJ = ROWS * 32 / NT;
-    int rtt[TJ], rpos[TJ];
-    float rfreq[TJ];
-    if (half_rot) {
-#pragma unroll
-        for (int j = 0; j < TJ; j++) {
-            const int idx = tid + NT * j, row = idx >> 5, i = idx & 31;
-            rtt[j] = trow[row];
-            rpos[j] = p.pos3[3 * (size_t)(rtt[j] >= 0 ? rtt[j] : 0) + i % 3];
-            rfreq[j] = p.inv_freq[i];
-        }
-    }
-    float wn[16];
-    if (p.k_norm) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 w4 = *(const float4 *)(p.k_norm + 16 * k + 4 * q);
-            wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
-        }
-    }
-    // A V element with |v| > f16_lim, or NaN, saturates to +-65536 (bf16's rounding of 65504)
-    // and flags the record, as split16 does for the reference's f16 V plane
-    // (metal/clef.metal:857-867): the same records are flagged for the FP32 rerun, and nothing
-    // past a record's own keys can read inf or NaN.
-    bool bad = false;
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            kw[h][j] = t >= 0 ? kw[h][j] : 0u;
-            unsigned w = t >= 0 ? vw[h][j] : 0u;
-            const bool lo_bad = !(__uint_as_float((w & 0x7fffu) << 16) <= p.f16_lim),
-                       hi_bad = !(__uint_as_float(w & 0x7fff0000u) <= p.f16_lim);
-            if (lo_bad) w = (w & 0xffff8000u) | 0x4780u;
-            if (hi_bad) w = (w & 0x8000ffffu) | 0x47800000u;
-            bad |= lo_bad | hi_bad;
-            vw[h][j] = w;
-        }
-    if (half_rot) {
-#pragma unroll
-        for (int j = 0; j < TJ; j++) {
-            const int idx = tid + NT * j, row = idx >> 5, i = idx & 31;
-            if (rtt[j] >= 0) {
-                const float ang = (float)rpos[j] * rfreq[j];
-                float sn, cn;
-                rope_sincos(ang, &sn, &cn);
-                csl[row][i] = make_float2(cn, sn);
-                if (p.rope_cs && kh == 0) *(float2 *)(p.rope_cs + (size_t)rtt[j] * 2 * half_rot + 2 * i) = make_float2(cn, sn);
-            }
-        }
-    }
-    // V rows into LDS, row-major
-    *(u32x4 *)(vl + rr * VS + 16 * k) = vw[0];
-    *(u32x4 *)(vl + rr * VS + 16 * k + 8) = vw[1];
-    __syncthreads();
-    float x[16];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        x[2 * j] = bf_lo(kw[0][j]);
-        x[2 * j + 1] = bf_hi(kw[0][j]);
-        x[8 + 2 * j] = bf_lo(kw[1][j]);
-        x[8 + 2 * j + 1] = bf_hi(kw[1][j]);
-    }
-    if (p.k_norm) {
-        float ss = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; e++) ss += x[e] * x[e];
-        ss = row16_sum(ss);
-        const float inv = rsqrtf(ss / (float)HD + p.eps);
-#pragma unroll
-        for (int e = 0; e < 16; e++) x[e] *= inv * wn[e];
-    }
-    if (half_rot) {
-        // lanes 0, 1 hold dims 0-31, lanes 2, 3 their partners 32-63 (two lanes apart)
-        float y[16];
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            // row_ror:n hands lane i the value of lane (i - n) mod 16
-            const float up = __builtin_amdgcn_update_dpp(0.f, x[e], 0x12e, 0xf, 0xf, false);   // lane + 2
-            const float dn = __builtin_amdgcn_update_dpp(0.f, x[e], 0x122, 0xf, 0xf, false);   // lane - 2
-            y[e] = (k & 2) ? dn : up;
-        }
-        if (k < 4) {
-            const bool first = k < 2;
-            const float2 *cs = csl[rr] + 16 * (k & 1);
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const float2 v = cs[e];
-                x[e] = first ? x[e] * v.x - y[e] * v.y : x[e] * v.x + y[e] * v.y;
-            }
-        }
-    }
-    // The f16 K plane follows split16: |k| > f16_lim or NaN saturates to +-65504 and flags the
-    // record (at its first pass row, seq_start).
-    {
-        const unsigned lim = __float_as_uint(p.f16_lim);
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const bool over = (__float_as_uint(x[e]) & 0x7fffffffu) > lim;
-            x[e] = over ? copysignf(65504.f, x[e]) : x[e];
-            bad |= over;
-        }
-    }
-    if (bad && t >= 0 && p.ovf && p.seq_start)
-        __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (t >= 0) {
-        uint16_t *dst = p.k_plane + ((size_t)kh * p.kvT + r0 + rr) * HD + 16 * k;
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const float *xs = x + 8 * h;
-            u32x4 ko = {pack_f16(xs[0], xs[1]), pack_f16(xs[2], xs[3]), pack_f16(xs[4], xs[5]), pack_f16(xs[6], xs[7])};
-            *(u32x4 *)(dst + 8 * h) = ko;
-        }
-    }
-    // V^T: wave w covers dims 64(w%4) .. +63 of rows 16(w/4) .. +15. In read q (rows
-    // 16(w/4) + 4q .. +3), lane s of 16-lane group g addresses row 16(w/4) + 4q + s/4, dims
-    // 64(w%4) + 16g + 4(s%4) .. +3, and receives dim 64(w%4) + 16g + s of the 4 rows.
-    const int g = lane >> 4, s16 = lane & 15, db = wave & 3, rg = wave >> 2;
-    const int d = 64 * db + 16 * g + s16;
-    const unsigned base = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) uint16_t *)vl;
-    short4_t rd[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const unsigned a = base + 2u * (unsigned)((16 * rg + 4 * q + (s16 >> 2)) * VS + 64 * db + 16 * g + 4 * (s16 & 3));
-        rd[q] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)(uintptr_t)a);
-    }
-#pragma unroll
-    for (int run = 0; run < 2; run++) {
-        const int rb = 16 * rg + 8 * run;
-        unsigned own = 0;
-#pragma unroll
-        for (int e = 0; e < 8; e++) own |= (trow[rb + e] >= 0 ? 1u : 0u) << e;
-        if (!own) continue;
-        const short4_t lo = rd[2 * run], hi = rd[2 * run + 1];
-        u32x4 w = {(unsigned)(uint16_t)lo[0] | ((unsigned)(uint16_t)lo[1] << 16), (unsigned)(uint16_t)lo[2] | ((unsigned)(uint16_t)lo[3] << 16),
-                   (unsigned)(uint16_t)hi[0] | ((unsigned)(uint16_t)hi[1] << 16), (unsigned)(uint16_t)hi[2] | ((unsigned)(uint16_t)hi[3] << 16)};
-        uint16_t *dst = p.vt_plane + ((size_t)kh * HD + d) * p.kvT + r0 + rb;
-        if (own != 0xffu) {   // keep the rows this pass does not own
-            const u32x4 old = *(const u32x4 *)dst;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const unsigned m = ((own >> (2 * j)) & 1u ? 0xffffu : 0u) | ((own >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
-                w[j] = (w[j] & m) | (old[j] & ~m);
-            }
-        }
-        *(u32x4 *)dst = w;
-    }
 }
 
 // ------------------------------------------------------------------------------------------

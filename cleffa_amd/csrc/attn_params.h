@@ -27,21 +27,6 @@ struct AttnParams {
     const int32_t *sched;     // NULL, or a schedule: header {magic, n_blk, nh, n_wg, nkv, fingerprint, 0, 0}, [n_wg + 1] offsets, items
 };
 
-struct PrepParams {
-    const uint16_t *qkv;
-    const float *k_norm;
-    const int32_t *pos3;
-    const float *inv_freq;
-    const int32_t *kv_tok;    // pass row of each plane row, -1: not written
-    uint16_t *k_plane;
-    uint16_t *vt_plane;
-    float *rope_cs;
-    const int32_t *seq_start; // record start of each pass row (overflow flags), or NULL
-    int32_t *ovf;
-    int kv_rows, row, nh, nkv, n_rot, kvT;
-    float eps, f16_lim;
-};
-
 struct VisPrepParams {
     const uint16_t *qkv;
     const float *bias;

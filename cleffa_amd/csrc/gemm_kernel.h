@@ -18,7 +18,7 @@
 //             accumulators are four consecutive columns of one output row.
 //   epilogue: accumulators rounded to bf16 into an LDS copy of the tile, then coalesced row
 //             stores; K and V tiles take the prologue from that copy, so their planes hold
-//             bitwise what text_prep_kv_kernel makes of the same bf16 rows.
+//             bitwise what text_prep_rows_kernel makes of the same bf16 rows (both run kv_rows.h).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -26,6 +26,7 @@
 #include <utility>
 
 #include "attn_kernels.h"
+#include "kv_rows.h"
 
 namespace clef_hip {
 namespace gemm {
@@ -41,18 +42,8 @@ struct Params {
     uint16_t *Y;              // [T][ldy] bf16
     int T, N, K, ldy;
     int m_tiles, n_tiles, n_per_xcd;   // n_per_xcd: the most N tiles any XCD owns
-    // fused K/V prologue (kv != 0): the QKV layout of the text path
-    int kv, nh, nkv, n_rot, kvT;
-    float eps, f16_lim;
-    const float *k_norm;      // [HD] or NULL
-    const int32_t *pos3;      // [T][3]
-    const float *inv_freq;    // [n_rot / 2]
-    const int32_t *tok_kv;    // [T]: plane row of each pass row's key
-    const int32_t *seq_start; // [T] or NULL
-    int32_t *ovf;             // [T] or NULL
-    uint16_t *k_plane;        // [nkv][kvT][HD] f16
-    uint16_t *vt_plane;       // [nkv][HD][kvT] bf16
-    float *rope_cs;           // [T][n_rot / 2][2] or NULL
+    int kv;                   // the fused K/V prologue: the QKV layout of the text path
+    KvRows r;
 };
 
 __device__ __forceinline__ unsigned lds_u32(const void *p) {
@@ -86,120 +77,6 @@ __device__ __forceinline__ bool tile_of(const Params &p, int b, int *tm, int *tn
     return true;
 }
 
-// The K/V prologue of one 128-row tile of a K head (kh) from the bf16 C tile in LDS: the
-// arithmetic of text_prep_kv_kernel (16 lanes per row, 16 dims per lane, the same operation
-// order), on pass rows instead of plane rows.
-template <int NTHREADS, int BM>
-__device__ __forceinline__ void k_epilogue(const Params &p, const uint8_t *ct, int m0, int kh) {
-    const int tid = threadIdx.x, rr = tid >> 4, k = tid & 15;
-    const int half_rot = p.n_rot / 2;
-    float wn[16];
-    if (p.k_norm) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 w4 = *(const float4 *)(p.k_norm + 16 * k + 4 * q);
-            wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
-        }
-    }
-    for (int pass = 0; pass < BM * 16 / NTHREADS; pass++) {
-        const int row = NTHREADS / 16 * pass + rr, t = m0 + row;
-        if (t >= p.T) break;   // rows are in order: the rest of this lane's rows are past T too
-        const u32x4 kw0 = *(const u32x4 *)(ct + row * CS + 32 * k), kw1 = *(const u32x4 *)(ct + row * CS + 32 * k + 16);
-        float x[16];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            x[2 * j] = bf_lo(kw0[j]);
-            x[2 * j + 1] = bf_hi(kw0[j]);
-            x[8 + 2 * j] = bf_lo(kw1[j]);
-            x[8 + 2 * j + 1] = bf_hi(kw1[j]);
-        }
-        float2 cs[16];
-        if (half_rot && k < 4) {   // lanes 0-3: pairs 16 (k & 1) .. +15 (lanes 2, 3 hold the partners)
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int i = 16 * (k & 1) + e;
-                const float ang = (float)p.pos3[3 * (size_t)t + i % 3] * p.inv_freq[i];
-                float sn, cn;
-                rope_sincos(ang, &sn, &cn);
-                cs[e] = make_float2(cn, sn);
-            }
-            if (p.rope_cs && kh == 0 && k < 2) {
-#pragma unroll
-                for (int e = 0; e < 16; e++) *(float2 *)(p.rope_cs + (size_t)t * 2 * half_rot + 2 * (16 * k + e)) = cs[e];
-            }
-        }
-        if (p.k_norm) {
-            float ss = 0.f;
-#pragma unroll
-            for (int e = 0; e < 16; e++) ss += x[e] * x[e];
-            ss = row16_sum(ss);
-            const float inv = rsqrtf(ss / (float)HD + p.eps);
-#pragma unroll
-            for (int e = 0; e < 16; e++) x[e] *= inv * wn[e];
-        }
-        if (half_rot) {
-            float y[16];
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const float up = __builtin_amdgcn_update_dpp(0.f, x[e], 0x12e, 0xf, 0xf, false);   // lane + 2
-                const float dn = __builtin_amdgcn_update_dpp(0.f, x[e], 0x122, 0xf, 0xf, false);   // lane - 2
-                y[e] = (k & 2) ? dn : up;
-            }
-            if (k < 4) {
-                const bool first = k < 2;
-#pragma unroll
-                for (int e = 0; e < 16; e++) x[e] = first ? x[e] * cs[e].x - y[e] * cs[e].y : x[e] * cs[e].x + y[e] * cs[e].y;
-            }
-        }
-        bool bad = false;
-        const unsigned lim = __float_as_uint(p.f16_lim);
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const bool over = (__float_as_uint(x[e]) & 0x7fffffffu) > lim;
-            x[e] = over ? copysignf(65504.f, x[e]) : x[e];
-            bad |= over;
-        }
-        if (bad && p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        uint16_t *dst = p.k_plane + ((size_t)kh * p.kvT + p.tok_kv[t]) * HD + 16 * k;
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const float *xs = x + 8 * h;
-            u32x4 ko = {pack_f16(xs[0], xs[1]), pack_f16(xs[2], xs[3]), pack_f16(xs[4], xs[5]), pack_f16(xs[6], xs[7])};
-            *(u32x4 *)(dst + 8 * h) = ko;
-        }
-    }
-}
-
-// V^T entries of one tile of a V head (kh): lane = pass row, so each store of a dim covers 64
-// consecutive plane rows of a record (2 bytes a lane). Only the pass's own plane rows are
-// written. Values with |v| > f16_lim or NaN saturate to +-65536 and flag the record, as in
-// text_prep_kv_kernel.
-template <int NWAVES, int BM>
-__device__ __forceinline__ void v_epilogue(const Params &p, const uint8_t *ct, int m0, int kh) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    // BM / 16 tasks: rows 64 (task % (BM / 64)) + lane, dims 64 (task / (BM / 64)) .. +63
-    constexpr int RB = BM / 64;
-    for (int task = tid >> 6; task < 4 * RB; task += NWAVES) {
-        const int row = 64 * (task % RB) + lane, t = m0 + row, d0 = 64 * (task / RB);
-        if (t >= p.T) continue;
-        const size_t prow = (size_t)p.tok_kv[t];
-        uint16_t *col = p.vt_plane + ((size_t)kh * HD + d0) * p.kvT + prow;
-        bool bad = false;
-#pragma unroll 8
-        for (int d = 0; d < 64; d += 2) {
-            unsigned w = *(const unsigned *)(ct + row * CS + 2 * (d0 + d));
-            const bool lo_bad = !(__uint_as_float((w & 0x7fffu) << 16) <= p.f16_lim),
-                       hi_bad = !(__uint_as_float(w & 0x7fff0000u) <= p.f16_lim);
-            if (lo_bad) w = (w & 0xffff8000u) | 0x4780u;
-            if (hi_bad) w = (w & 0x8000ffffu) | 0x47800000u;
-            bad |= lo_bad | hi_bad;
-            col[(size_t)d * p.kvT] = (uint16_t)w;
-            col[(size_t)(d + 1) * p.kvT] = (uint16_t)(w >> 16);
-        }
-        if (bad && p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
 // Kernel configuration: WM x WN output block per wave ((BM / WM) x (BN / WN) waves), K slices
 // of BK (32 or 64) staged STAGES deep in LDS.
 template <int BM_, int WM_, int WN_, int BK_, int STAGES_>
@@ -209,7 +86,9 @@ struct Cfg {
     static constexpr int MT = WM / 16, NT = WN / 16, FR = MT + NT;   // 16-row / 16-column fragments
     static constexpr int KS = BK / 32;                               // 32-deep product steps per slice
     static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2, STAGE_BYTES = A_BYTES + B_BYTES;
-    static constexpr int LDS_BYTES = STAGES * STAGE_BYTES > BM * CS ? STAGES * STAGE_BYTES : BM * CS;
+    // the stages, or the C tile and the rotary table of the K rows' epilogue (kv_rows.h)
+    static constexpr int EPI_BYTES = BM * CS + THREADS / 16 * 32 * 8;
+    static constexpr int LDS_BYTES = STAGES * STAGE_BYTES > EPI_BYTES ? STAGES * STAGE_BYTES : EPI_BYTES;
     static constexpr int CH = BK / 8;                  // 16-byte chunks per LDS row
     static constexpr int RPI = 1024 / (2 * BK);        // rows per 1 KB fill instruction
     static constexpr int R256 = 256 / (2 * BK);        // rows per 256 bytes (one pass over the banks)
@@ -368,9 +247,10 @@ __global__ __launch_bounds__(C::THREADS, 1) void qkv_gemm_kernel(Params p) {
             *(u32x4 *)(p.Y + (size_t)(m0 + row) * p.ldy + n0 + 8 * c16) = *(const u32x4 *)(lds + row * CS + 16 * c16);
     }
     if (p.kv) {
-        const int kcol = 2 * p.nh * HD;
-        if (n0 >= kcol && n0 < kcol + p.nkv * HD) k_epilogue<C::THREADS, BM>(p, lds, m0, (n0 - kcol) / HD);
-        else if (n0 >= kcol + p.nkv * HD) v_epilogue<C::WAVES, BM>(p, lds, m0, (n0 - kcol - p.nkv * HD) / HD);
+        const int kcol = 2 * p.r.nh * HD;
+        float2 *table = (float2 *)(lds + BM * CS);
+        if (n0 >= kcol && n0 < kcol + p.r.nkv * HD) k_rows<C::THREADS, BM>(p.r, lds, CS, m0, (n0 - kcol) / HD, table);
+        else if (n0 >= kcol + p.r.nkv * HD) v_rows<C::WAVES, BM>(p.r, lds, CS, m0, (n0 - kcol - p.r.nkv * HD) / HD);
     }
 }
 

@@ -1,0 +1,179 @@
+// The text path's K/V prologue on a tile of pass rows held in LDS (bf16, row stride cs bytes):
+// K rows are RMS-normalised, rotated (partial NeoX rotary, interleaved M-RoPE angles) and split
+// to the f16 K plane; V rows go to the V^T plane. Semantics: metal/clef.metal:245-300 (attn_prep
+// K and V) and 857-928 (split16 and attn_prep_split: the f16 planes, |x| > f16_lim or NaN
+// saturating and flagging the record).
+//
+// Two producers fill the tile: text_prep_rows_kernel (attn_kernels.h) loads it from the qkv
+// rows, and the QKV GEMM (gemm_kernel.h) leaves its bf16 output tile there; both then call these
+// functions, so the planes they write are bitwise the same.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attn_kernels.h"
+
+namespace clef_hip {
+
+struct KvRows {
+    int T, nh, nkv, n_rot, kvT;
+    float eps, f16_lim;
+    const float *k_norm;      // [256] or NULL
+    const int32_t *pos3;      // [T][3]
+    const float *inv_freq;    // [n_rot / 2]
+    const int32_t *tok_kv;    // [T]: plane row of each pass row's key
+    const int32_t *seq_start; // [T] or NULL
+    int32_t *ovf;             // [T] or NULL
+    uint16_t *k_plane;        // [nkv][kvT][256] f16
+    uint16_t *vt_plane;       // [nkv][256][kvT] bf16
+    float *rope_cs;           // [T][n_rot / 2][2] or NULL
+};
+
+// K rows m0 .. m0 + BM - 1 of kv head kh (those below T): 16 lanes per row, 16 dims per lane,
+// NTHREADS / 16 rows per pass. Each pass first computes the rotary cos/sin of its rows, two
+// pairs per lane, into `table` (LDS, [NTHREADS / 16][32] float2), and kv head 0 stores them in
+// rope_cs for the Q prologue. Every thread runs every pass (the table needs two barriers).
+template <int NTHREADS, int BM>
+__device__ __forceinline__ void k_rows(const KvRows &p, const uint8_t *ct, int cs, int m0, int kh, float2 *table) {
+    constexpr int HD = 256, RPP = NTHREADS / 16;
+    const int tid = threadIdx.x, rr = tid >> 4, k = tid & 15;
+    const int half_rot = p.n_rot / 2;   // 0 or 32: dims [0, 32) pair with [32, 64)
+    float wn[16];
+    if (p.k_norm) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 w4 = *(const float4 *)(p.k_norm + 16 * k + 4 * q);
+            wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
+        }
+    }
+    for (int pass = 0; pass < BM / RPP; pass++) {
+        const int row = RPP * pass + rr, t = m0 + row;
+        const bool valid = t < p.T;
+        if (half_rot) {
+            if (valid) {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int i = 2 * k + h;
+                    const float ang = (float)p.pos3[3 * (size_t)t + i % 3] * p.inv_freq[i];
+                    float sn, cn;
+                    rope_sincos(ang, &sn, &cn);
+                    table[32 * rr + i] = make_float2(cn, sn);
+                    if (p.rope_cs && kh == 0) *(float2 *)(p.rope_cs + (size_t)t * 2 * half_rot + 2 * i) = make_float2(cn, sn);
+                }
+            }
+            __syncthreads();
+        }
+        if (valid) {
+            const u32x4 kw0 = *(const u32x4 *)(ct + row * cs + 32 * k), kw1 = *(const u32x4 *)(ct + row * cs + 32 * k + 16);
+            float x[16];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                x[2 * j] = bf_lo(kw0[j]);
+                x[2 * j + 1] = bf_hi(kw0[j]);
+                x[8 + 2 * j] = bf_lo(kw1[j]);
+                x[8 + 2 * j + 1] = bf_hi(kw1[j]);
+            }
+            if (p.k_norm) {
+                float ss = 0.f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) ss += x[e] * x[e];
+                ss = row16_sum(ss);
+                const float inv = rsqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+                for (int e = 0; e < 16; e++) x[e] *= inv * wn[e];
+            }
+            if (half_rot) {
+                // lanes 0, 1 hold dims 0-31, lanes 2, 3 their partners 32-63 (two lanes apart)
+                float y[16];
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const float up = __builtin_amdgcn_update_dpp(0.f, x[e], 0x12e, 0xf, 0xf, false);   // lane + 2
+                    const float dn = __builtin_amdgcn_update_dpp(0.f, x[e], 0x122, 0xf, 0xf, false);   // lane - 2
+                    y[e] = (k & 2) ? dn : up;
+                }
+                if (k < 4) {
+                    const bool first = k < 2;
+                    const float2 *c = table + 32 * rr + 16 * (k & 1);
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const float2 v = c[e];
+                        x[e] = first ? x[e] * v.x - y[e] * v.y : x[e] * v.x + y[e] * v.y;
+                    }
+                }
+            }
+            bool bad = false;
+            const unsigned lim = __float_as_uint(p.f16_lim);
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const bool over = (__float_as_uint(x[e]) & 0x7fffffffu) > lim;
+                x[e] = over ? copysignf(65504.f, x[e]) : x[e];
+                bad |= over;
+            }
+            if (bad && p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint16_t *dst = p.k_plane + ((size_t)kh * p.kvT + p.tok_kv[t]) * HD + 16 * k;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float *xs = x + 8 * h;
+                u32x4 ko = {pack_f16(xs[0], xs[1]), pack_f16(xs[2], xs[3]), pack_f16(xs[4], xs[5]), pack_f16(xs[6], xs[7])};
+                *(u32x4 *)(dst + 8 * h) = ko;
+            }
+        }
+        if (half_rot) __syncthreads();   // the table is read before the next pass rewrites it
+    }
+}
+
+// V^T entries of rows m0 .. m0 + BM - 1 of kv head kh: lane = pass row, so each store of one
+// dim covers 64 consecutive plane rows of a record (2 bytes a lane, one 128-byte line); only the
+// pass's own plane rows are written. The NWAVES waves split the tile into (row block of 64,
+// dim range) tasks. Values with |v| > f16_lim or NaN saturate to +-65536 (bf16's rounding of
+// 65504) and flag the record.
+template <int NWAVES, int BM>
+__device__ __forceinline__ void v_rows(const KvRows &p, const uint8_t *ct, int cs, int m0, int kh) {
+    constexpr int HD = 256, RB = BM / 64;
+    constexpr int TASKS = NWAVES > RB ? NWAVES : RB, DPT = HD * RB / TASKS;   // dims per task
+    static_assert(DPT % 2 == 0 && HD * RB % TASKS == 0, "tasks split the dims evenly");
+    const int tid = threadIdx.x, lane = tid & 63;
+    for (int task = tid >> 6; task < TASKS; task += NWAVES) {
+        const int row = 64 * (task % RB) + lane, t = m0 + row, d0 = DPT * (task / RB);
+        if (t >= p.T) continue;
+        uint16_t *col = p.vt_plane + ((size_t)kh * HD + d0) * p.kvT + (size_t)p.tok_kv[t];
+        bool bad = false;
+#pragma unroll 8
+        for (int d = 0; d < DPT; d += 2) {
+            unsigned w = *(const unsigned *)(ct + row * cs + 2 * (d0 + d));
+            const bool lo_bad = !(__uint_as_float((w & 0x7fffu) << 16) <= p.f16_lim),
+                       hi_bad = !(__uint_as_float(w & 0x7fff0000u) <= p.f16_lim);
+            if (lo_bad) w = (w & 0xffff8000u) | 0x4780u;
+            if (hi_bad) w = (w & 0x8000ffffu) | 0x47800000u;
+            bad |= lo_bad | hi_bad;
+            col[(size_t)d * p.kvT] = (uint16_t)w;
+            col[(size_t)(d + 1) * p.kvT] = (uint16_t)(w >> 16);
+        }
+        if (bad && p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// The K/V prologue as its own kernel, over pass rows: workgroup (b, j) loads rows 64b .. 64b + 63
+// of K head j (j < nkv) or V head j - nkv into LDS and runs k_rows / v_rows on them. All loads
+// are issued at once (no load depends on another), and the plane rows come from tok_kv.
+constexpr int kPrepRowsBM = 64, kPrepRowsThreads = 512, kPrepRowsCS = 512 + 16;
+__global__ __launch_bounds__(kPrepRowsThreads) void text_prep_rows_kernel(const uint16_t *qkv, int row_len, KvRows p) {
+    constexpr int BM = kPrepRowsBM, NT = kPrepRowsThreads, CSB = kPrepRowsCS;
+    __shared__ __attribute__((aligned(16))) uint8_t tile[BM * CSB];
+    __shared__ __attribute__((aligned(16))) float2 table[NT / 16 * 32];
+    const int tid = threadIdx.x, m0 = blockIdx.x * BM, j = blockIdx.y;
+    const bool is_k = j < p.nkv;
+    const int head = is_k ? j : j - p.nkv;
+    const uint16_t *src = qkv + (size_t)p.nh * 2 * 256 + (size_t)(is_k ? 0 : p.nkv * 256) + (size_t)head * 256;
+#pragma unroll
+    for (int i = 0; i < BM * 32 / NT; i++) {
+        const int id = tid + NT * i, r = id >> 5, c16 = id & 31;
+        const int t = min(m0 + r, p.T - 1);
+        *(u32x4 *)(tile + r * CSB + 16 * c16) = *(const u32x4 *)(src + (size_t)t * row_len + 8 * c16);
+    }
+    __syncthreads();
+    if (is_k) k_rows<NT, BM>(p, tile, CSB, m0, head, table);
+    else v_rows<NT / 64, BM>(p, tile, CSB, m0, head);
+}
+
+}  // namespace clef_hip

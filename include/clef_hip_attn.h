@@ -107,7 +107,8 @@ typedef struct {
     int kvT;                  /* rows per head of the planes: >= plan kv_rows, multiple of 8 */
     const int32_t *blocks;    /* device copy of the plan's blocks */
     int n_blk;
-    const int32_t *kv_tok;    /* device copy of the plan's kv_tok [kv_rows] */
+    const int32_t *kv_tok;    /* device copy of the plan's kv_tok [kv_rows] (the FP32 prologue runs
+                                 over plane rows with it) */
     int kv_rows;              /* the plan's kv_rows */
     int causal;               /* 1 for the text models */
     int gate;                 /* 1: multiply by sigmoid(gate) (Qwen3.5 gated attention) */
@@ -147,6 +148,8 @@ typedef struct {
                                  an overflow (clef.c:526-550) and CLEF_ATTN_TU=0. In FP32 mode nh /
                                  nkv must be at most 8, sched and trace are ignored, and only the
                                  output (f16 out_type) can flag. Other values are rejected */
+    const int32_t *tok_kv;    /* [T] device int32: the plan's pass row -> plane row map (the inverse
+                                 of kv_tok); the bf16 K/V prologue runs over pass rows with it */
 } clef_hip_attn_args;
 
 #define CLEF_HIP_QKV_BF16 0
@@ -187,9 +190,10 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
 bool clef_hip_qkv_gemm(int H, const uint16_t *X, const uint16_t *W, const clef_hip_attn_args *a, const int32_t *tok_kv,
                        void *stream, char *err, size_t errlen);
 
-/* K/V prologue only: RMSNorm + rotary of each pass row's K into its plane row (kv_tok), V into
+/* K/V prologue only: RMSNorm + rotary of each pass row's K into its plane row (tok_kv; kv_tok in
+ * FP32 mode), V into
  * the V^T plane (attn_prep / attn_prep_split / attn_prep_prefix K and V parts,
- * metal/clef.metal:245-300, 657-707, 873-928). Plane rows with kv_tok -1 are not written. */
+ * metal/clef.metal:245-300, 657-707, 873-928). Plane rows no pass row maps to are not written. */
 bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen);
 /* Attention core with the Q prologue and gate epilogue fused (attention_tu and the FP32
  * kernels, metal/clef.metal:316-654, 709-849, 930-1093). Reads the planes prep_kv wrote. */

@@ -20,7 +20,7 @@ int main(void) {
     F(clef_hip_attn_args, causal); F(clef_hip_attn_args, gate); F(clef_hip_attn_args, out);
     F(clef_hip_attn_args, out_type); F(clef_hip_attn_args, f16_lim); F(clef_hip_attn_args, ovf);
     F(clef_hip_attn_args, trace); F(clef_hip_attn_args, sched); F(clef_hip_attn_args, n_wg);
-    F(clef_hip_attn_args, seq_start); F(clef_hip_attn_args, qkv_type);
+    F(clef_hip_attn_args, seq_start); F(clef_hip_attn_args, qkv_type); F(clef_hip_attn_args, tok_kv);
     Z(clef_hip_attn_args);
 
     F(clef_hip_vis_args, P); F(clef_hip_vis_args, heads); F(clef_hip_vis_args, hd);

@@ -80,7 +80,7 @@ int main(int argc, char **argv) {
     clef_hip_rope_inv_freq(1e7f, NROT, inv_freq);
 
     /* device buffers */
-    void *d_qkv, *d_qn, *d_kn, *d_pos, *d_inv, *d_cs, *d_k, *d_vt, *d_blk, *d_kvtok, *d_ss, *d_out, *d_ovf;
+    void *d_qkv, *d_qn, *d_kn, *d_pos, *d_inv, *d_cs, *d_k, *d_vt, *d_blk, *d_kvtok, *d_tokkv, *d_ss, *d_out, *d_ovf;
     CK(hipMalloc(&d_qkv, (size_t)T * row * 2));
     CK(hipMalloc(&d_qn, HD * 4));
     CK(hipMalloc(&d_kn, HD * 4));
@@ -91,6 +91,7 @@ int main(int argc, char **argv) {
     CK(hipMalloc(&d_vt, (size_t)NKV * kvT * HD * 2));
     CK(hipMalloc(&d_blk, (size_t)n_blk * CLEF_HIP_BLOCK_INTS * 4));
     CK(hipMalloc(&d_kvtok, (size_t)kv_rows * 4));
+    CK(hipMalloc(&d_tokkv, (size_t)T * 4));
     CK(hipMalloc(&d_ss, (size_t)T * 4));
     CK(hipMalloc(&d_out, (size_t)T * NH * HD * 2));
     CK(hipMalloc(&d_ovf, (size_t)T * 4));
@@ -101,6 +102,7 @@ int main(int argc, char **argv) {
     CK(hipMemcpy(d_inv, inv_freq, sizeof inv_freq, hipMemcpyHostToDevice));
     CK(hipMemcpy(d_blk, blocks, (size_t)n_blk * CLEF_HIP_BLOCK_INTS * 4, hipMemcpyHostToDevice));
     CK(hipMemcpy(d_kvtok, kv_tok, (size_t)kv_rows * 4, hipMemcpyHostToDevice));
+    CK(hipMemcpy(d_tokkv, tok_kv, (size_t)T * 4, hipMemcpyHostToDevice));
     CK(hipMemcpy(d_ss, seq_start, (size_t)T * 4, hipMemcpyHostToDevice));
     CK(hipMemset(d_ovf, 0, (size_t)T * 4));
 
@@ -109,7 +111,7 @@ int main(int argc, char **argv) {
     a.nh = NH; a.nkv = NKV; a.hd = HD; a.n_rot = NROT; a.eps = 1e-6f; a.scale = 1.0f / 16.0f;
     a.T = T; a.row = row; a.qkv = d_qkv; a.q_norm = d_qn; a.k_norm = d_kn; a.pos3 = d_pos;
     a.inv_freq = d_inv; a.rope_cs = d_cs; a.k_plane = d_k; a.vt_plane = d_vt; a.kvT = kvT;
-    a.blocks = d_blk; a.n_blk = n_blk; a.kv_tok = d_kvtok; a.kv_rows = kv_rows; a.causal = 1;
+    a.blocks = d_blk; a.n_blk = n_blk; a.kv_tok = d_kvtok; a.tok_kv = d_tokkv; a.kv_rows = kv_rows; a.causal = 1;
     a.gate = 1; a.out = d_out; a.out_type = CLEF_HIP_OUT_BF16; a.f16_lim = 65504.0f; a.ovf = d_ovf;
     a.seq_start = d_ss; a.qkv_type = CLEF_HIP_QKV_BF16;
     uint16_t *out = malloc((size_t)T * NH * HD * 2);
