@@ -80,7 +80,6 @@ bool check_text(const clef_hip_attn_args *a, bool need_core, char *err, size_t e
         return fail(err, errlen, "qkv_type %d not supported: the qkv rows must be bf16 or f32", a->qkv_type);
     const bool f32 = a->qkv_type == CLEF_HIP_QKV_F32;
     if (a->nh <= 0 || a->nkv <= 0 || a->nh % a->nkv) return fail(err, errlen, "bad head counts nh=%d nkv=%d", a->nh, a->nkv);
-    if (f32 && a->nh / a->nkv > 8) return fail(err, errlen, "FP32 mode takes at most 8 q heads per kv head (got %d)", a->nh / a->nkv);
     if (!rot_ok(a->n_rot, a->hd)) return fail(err, errlen, "unsupported n_rot %d", a->n_rot);
     if (a->T < 0 || a->n_blk < 0 || a->kv_rows < 0) return fail(err, errlen, "negative sizes");
     const long need_row = 2L * a->nh * a->hd + 2L * a->nkv * a->hd;
@@ -181,7 +180,8 @@ bool vis_run(const clef_hip_vis_args *a, uint16_t *q_plane, uint16_t *k_plane, u
     return launch_ok("attn_vis", err, errlen);
 }
 
-// The FP32 core: text32::SUB workgroups of nh / nkv waves per (plan block, kv head).
+// The FP32 core over the (16-row sub-block, kv head, head chunk) items, W waves per workgroup
+// (the kernel's 130 KB of LDS allow one workgroup per CU).
 template <int W>
 void launch_f32(const text32::Params &p, long grid, hipStream_t s) {
     hipLaunchKernelGGL(text32::attn_text_f32_kernel<W>, dim3((unsigned)grid), dim3(64 * W), 0, s, p);
@@ -196,10 +196,23 @@ bool core_f32(const clef_hip_attn_args *a, void *stream, char *err, size_t errle
     p.row = a->row; p.kvT = a->kvT; p.nh = a->nh; p.nkv = a->nkv; p.n_rot = a->n_rot;
     p.causal = a->causal ? 1 : 0; p.gate = a->gate ? 1 : 0; p.out_type = a->out_type;
     p.eps = a->eps; p.scale = a->scale; p.f16_lim = f16_limit(a->f16_lim);
-    const long grid = (long)a->n_blk * text32::SUB * a->nkv;
-    if (grid > 0x7fffffffL) return fail(err, errlen, "grid too large");
+    // a kv group of G q heads runs as ceil(G / 8) chunks of W = ceil(G / chunks) heads
+    const int group = a->nh / a->nkv;
+    p.n_chunks = (group + 7) / 8;
+    const int W = (group + p.n_chunks - 1) / p.n_chunks;
+    p.n_blk = a->n_blk;
+    const long n_items = (long)a->n_blk * text32::SUB * a->nkv * p.n_chunks;
+    if (n_items > 0x7fffffffL) return fail(err, errlen, "grid too large");
+    // One workgroup per item, dispatched in the items' longest-first order: the hardware hands
+    // each free CU the next item, which balanced C1 better (594 us) than a persistent grid of
+    // one workgroup per CU over a static snake order (660 us; C2 within 1%).
+    // CLEF_HIP_F32_PERSISTENT=1 selects the persistent grid.
+    long grid = n_items;
+    const char *ge = getenv("CLEF_HIP_F32_PERSISTENT");
+    const long cus = device_cus();
+    if (ge && ge[0] == '1' && cus > 0 && cus < n_items) grid = cus;
     hipStream_t s = (hipStream_t)stream;
-    switch (a->nh / a->nkv) {
+    switch (W) {
         case 1: launch_f32<1>(p, grid, s); break;
         case 2: launch_f32<2>(p, grid, s); break;
         case 3: launch_f32<3>(p, grid, s); break;

@@ -14,8 +14,9 @@
 // accumulation), the softmax in FP32 VALU. Key tiles start at the record's first key, so a
 // record's arithmetic does not depend on what is packed with it.
 //
-// Workgroup: one wave per q head of a GQA group (W = nh / nkv waves), all on the same 16 query
-// rows, so one 32-key K / V tile in LDS (64 KB, double buffered: 128 KB) serves the group.
+// Workgroup: one wave per q head of a chunk of the GQA group (W <= 8 waves; a group of more
+// than 8 heads runs as several chunks), all on the same 16 query rows, so one 32-key K / V tile
+// in LDS (64 KB, double buffered: 128 KB) serves the chunk.
 //   S^T = K . Q^T      A = 16 keys x 4 dims of K (LDS), B = the wave's Q (registers).
 //   O^T += V^T . P^T   A = 16 dims x 4 keys of V (LDS), B = P (registers).
 // Lane l = 16 g + r. S^T's A row r takes key 4(r % 4) + r / 4 of the 16-key subtile, so the four
@@ -76,6 +77,7 @@ struct Params {
     void *out;
     int32_t *ovf;
     int row, kvT, nh, nkv, n_rot, causal, gate, out_type;
+    int n_blk, n_chunks;        // plan blocks; head chunks per kv group (ceil(group / 8))
     float eps, scale, f16_lim;
 };
 
@@ -154,32 +156,61 @@ __device__ __forceinline__ void sfor(F &&f) {
     sfor_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// Grid: SUB workgroups per (plan block, kv head), block-major, each block's last rows first; wave w
-// is q head kh * W + w.
+// Work items are (16-row sub-block, kv head, head chunk): the kv group's G = nh / nkv q heads
+// split into n_chunks chunks of at most W <= 8 heads, one wave per head (a chunk's spare waves
+// fill tiles and take barriers but compute nothing). Items run in the plan's longest-first
+// block order, each block's last 16 rows (its longest causal rows) first. With G workgroups,
+// workgroup b takes items b, then 2G - 1 - b, ... (snake order, so long and short items mix;
+// one item each when G is the item count); while an item's epilogue runs, the next item's
+// first K / V tile loads into the idle LDS buffers.
 template <int W>
 __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) float smem[4 * TILE];   // K0 | K1 | V0 | V1
-    const int kh = blockIdx.x % p.nkv, sb = blockIdx.x / p.nkv;
-    // the block's last 16 rows (its longest causal rows) first: blocks come longest first
-    const int bi = sb / SUB, sub = SUB - 1 - sb % SUB;
-    const int32_t *blk = p.blocks + 8 * bi;
-    const int nq = min(BQ, blk[1] - BQ * sub);
-    if (nq <= 0) return;                                  // workgroup-uniform
-    const int q_row0 = blk[0] + BQ * sub, q_pos0 = blk[2] + BQ * sub, k_row0 = blk[3];
-    const int k_len = p.causal ? min(blk[4], q_pos0 + nq) : blk[4];
-    int32_t *flag = p.ovf ? p.ovf + blk[5] : nullptr;
-    const int n_tiles = (k_len + BK - 1) / BK;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int r16 = lane & 15, g = lane >> 4;
-    const int h = kh * W + wave;
-    const bool q_valid = r16 < nq;
-    const int qpos = q_pos0 + r16;
-    const int t = q_row0 + (q_valid ? r16 : 0);
+    const int group = p.nh / p.nkv;
+    const int n_items = p.n_blk * SUB * p.nkv * p.n_chunks;
+    const int G = gridDim.x;
+    struct Item {
+        int nq, q_row0, q_pos0, k_row0, k_len, n_tiles, kh, h;
+        bool live;   // this wave has a head in the item's chunk
+        int32_t *flag;
+    };
+    // the k-th item of this workgroup, or nq = 0 past the end
+    auto item_at = [&](int k, Item &it) {
+        const int j = k * G + ((k & 1) ? G - 1 - (int)blockIdx.x : (int)blockIdx.x);
+        it.nq = 0;
+        if (j >= n_items) return false;
+        const int chunk = j % p.n_chunks, rest = j / p.n_chunks;
+        it.kh = rest % p.nkv;
+        const int sb = rest / p.nkv, bi = sb / SUB, sub = SUB - 1 - sb % SUB;
+        const int32_t *blk = p.blocks + 8 * bi;
+        it.nq = min(BQ, blk[1] - BQ * sub);
+        if (it.nq <= 0) { it.nq = 0; return true; }      // a sub-block past the block's rows
+        it.q_row0 = blk[0] + BQ * sub;
+        it.q_pos0 = blk[2] + BQ * sub;
+        it.k_row0 = blk[3];
+        it.k_len = p.causal ? min(blk[4], it.q_pos0 + it.nq) : blk[4];
+        it.n_tiles = (it.k_len + BK - 1) / BK;
+        it.flag = p.ovf ? p.ovf + blk[5] : nullptr;
+        const int hw = chunk * W + wave;
+        it.live = hw < group;
+        it.h = it.kh * group + (it.live ? hw : 0);
+        return true;
+    };
+    // next item with rows, from ordinal k on; false past the end
+    auto advance = [&](int &k, Item &it) {
+        while (item_at(k, it)) {
+            if (it.nq > 0) return true;
+            k++;
+        }
+        return false;
+    };
 
     // ---- tile fills: one 1 KB DMA group per key row; wave w fills rows w, w + W, ...
-    const float *kbase = p.k_plane + ((size_t)kh * p.kvT + k_row0) * HD;
-    const float *vbase = p.v_plane + ((size_t)kh * p.kvT + k_row0) * HD;
-    auto fill = [&](int kb, float *Ks, float *Vs) {
+    auto fill = [&](const Item &it, int kb, float *Ks, float *Vs) {
+        const float *kbase = p.k_plane + ((size_t)it.kh * p.kvT + it.k_row0) * HD;
+        const float *vbase = p.v_plane + ((size_t)it.kh * p.kvT + it.k_row0) * HD;
         for (int r = wave; r < BK; r += W) {
             const size_t off = (size_t)(kb + r) * HD + 4 * lane;
             __builtin_amdgcn_global_load_lds((const void *)(kbase + off), (lds_void *)(Ks + r * ROW), 16, 0, 0);
@@ -188,10 +219,10 @@ __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
     };
     // Rows past the keys (not written by this pass, possibly not finite) -> 0 in V, so that the
     // zero probabilities of masked keys give exact zero products.
-    auto clear_tail = [&](int kb, float *Vs) {
-        if (kb + BK <= k_len) return;                     // workgroup-uniform
+    auto clear_tail = [&](const Item &it, int kb, float *Vs) {
+        if (kb + BK <= it.k_len) return;                  // workgroup-uniform
         for (int r = wave; r < BK; r += W)
-            if (kb + r >= k_len) *(f32x4 *)(Vs + r * ROW + 4 * lane) = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (kb + r >= it.k_len) *(f32x4 *)(Vs + r * ROW + 4 * lane) = f32x4{0.f, 0.f, 0.f, 0.f};
     };
 
     const unsigned lds0 = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) float *)smem;
@@ -199,173 +230,193 @@ __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
     const unsigned ka = lds0 + (unsigned)(4 * (r16 & 3) + (r16 >> 2)) * ROW * 4u + 256u * g;
     const unsigned va = lds0 + 2u * TB + (unsigned)g * ROW * 4u + 16u * r16;
 
-    if (n_tiles > 0) fill(0, smem, smem + 2 * TILE);
+    int k = 0;
+    Item cur;
+    if (!advance(k, cur)) return;
+    if (cur.n_tiles > 0) fill(cur, 0, smem, smem + 2 * TILE);
+    for (;;) {
+        const bool q_valid = r16 < cur.nq;
+        const int qpos = cur.q_pos0 + r16;
+        const int t = cur.q_row0 + (q_valid ? r16 : 0);
+        const int h = cur.h;
+        const int k_len = cur.k_len, n_tiles = cur.n_tiles;
 
-    // ---- Q prologue: lane holds Q[row r16][64 g + c], normalised and rotated, FP32
-    float qf[64];
-    {
-        const f32x4 *qs = (const f32x4 *)(p.qkv + (size_t)t * p.row + (size_t)h * 2 * HD + 64 * g);
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const f32x4 v = qs[j];
-            qf[4 * j] = v.x; qf[4 * j + 1] = v.y; qf[4 * j + 2] = v.z; qf[4 * j + 3] = v.w;
-        }
-        if (p.q_norm) {
-            float ss = 0.f;
-#pragma unroll
-            for (int c = 0; c < 64; c++) ss += qf[c] * qf[c];
-            ss += __shfl_xor(ss, 16);
-            ss += __shfl_xor(ss, 32);
-            const float inv = 1.0f / sqrtf(ss / (float)HD + p.eps);
-            const f32x4 *w = (const f32x4 *)(p.q_norm + 64 * g);
+        // ---- Q prologue: lane holds Q[row r16][64 g + c], normalised and rotated, FP32
+        float qf[64];
+        {
+            const f32x4 *qs = (const f32x4 *)(p.qkv + (size_t)t * p.row + (size_t)h * 2 * HD + 64 * g);
 #pragma unroll
             for (int j = 0; j < 16; j++) {
-                const f32x4 wv = w[j];
+                const f32x4 v = qs[j];
+                qf[4 * j] = v.x; qf[4 * j + 1] = v.y; qf[4 * j + 2] = v.z; qf[4 * j + 3] = v.w;
+            }
+            if (p.q_norm) {
+                float ss = 0.f;
 #pragma unroll
-                for (int e = 0; e < 4; e++) qf[4 * j + e] = qf[4 * j + e] * inv * wv[e];
+                for (int c = 0; c < 64; c++) ss += qf[c] * qf[c];
+                ss += __shfl_xor(ss, 16);
+                ss += __shfl_xor(ss, 32);
+                const float inv = 1.0f / sqrtf(ss / (float)HD + p.eps);
+                const f32x4 *w = (const f32x4 *)(p.q_norm + 64 * g);
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const f32x4 wv = w[j];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) qf[4 * j + e] = qf[4 * j + e] * inv * wv[e];
+                }
+            }
+            if (p.n_rot && g == 0) {
+#pragma unroll
+                for (int i = 0; i < 32; i++) {
+                    float c, s;
+                    if (p.rope_cs) {
+                        const float2 cs = *(const float2 *)(p.rope_cs + ((size_t)t * 32 + i) * 2);
+                        c = cs.x; s = cs.y;
+                    } else {
+                        rope_cs_f32(p.pos3, p.inv_freq, t, i, &c, &s);
+                    }
+                    const float x0 = qf[i], x1 = qf[i + 32];
+                    qf[i] = x0 * c - x1 * s;
+                    qf[i + 32] = x1 * c + x0 * s;
+                }
             }
         }
-        if (p.n_rot && g == 0) {
-#pragma unroll
-            for (int i = 0; i < 32; i++) {
-                float c, s;
-                if (p.rope_cs) {
-                    const float2 cs = *(const float2 *)(p.rope_cs + ((size_t)t * 32 + i) * 2);
-                    c = cs.x; s = cs.y;
-                } else {
-                    rope_cs_f32(p.pos3, p.inv_freq, t, i, &c, &s);
-                }
-                const float x0 = qf[i], x1 = qf[i + 32];
-                qf[i] = x0 * c - x1 * s;
-                qf[i + 32] = x1 * c + x0 * s;
-            }
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    if (n_tiles > 0) clear_tail(0, smem + 2 * TILE);
-    __syncthreads();
-
-    f32x4 o[16];
-#pragma unroll
-    for (int n = 0; n < 16; n++) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
-
-    auto tile = [&](const int ti, auto BUF) {
-        constexpr int buf = decltype(BUF)::value;
-        const int kb = ti * BK;
-        if (ti + 1 < n_tiles) fill(kb + BK, smem + (buf ^ 1) * TILE, smem + 2 * TILE + (buf ^ 1) * TILE);
-        // S^T: two 16-key subtiles, 64 four-dim steps each, their products interleaved (two
-        // independent accumulator chains); K read in runs of RUN chunks per subtile
-        f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-        sfor<NRUN>([&](auto H) {
-            constexpr int hh = decltype(H)::value;
-            f32x4 a[2][RUN];
-            sfor<RUN>([&](auto J) {
-                constexpr int j = decltype(J)::value;
-                a[0][j] = lds_read_f4<buf * TB + (RUN * hh + j) * 16>(ka);
-                a[1][j] = lds_read_f4<buf * TB + 16 * ROW * 4 + (RUN * hh + j) * 16>(ka);
-            });
-            sfor<RUN>([&](auto J) {
-                constexpr int j = decltype(J)::value;
-                lds_wait_f4<2 * (RUN - 1 - j) + 1>(a[0][j]);
-                lds_wait_f4<2 * (RUN - 1 - j)>(a[1][j]);
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    s[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0][j][e], qf[4 * (RUN * hh + j) + e], s[0], 0, 0, 0);
-                    s[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1][j][e], qf[4 * (RUN * hh + j) + e], s[1], 0, 0, 0);
-                }
-            });
-        });
-        // V chunk j of step st = (u, v): key 16u + 4v + g, chunk 16j + r16 of its row
-        auto vread = [&](auto ST, auto J) {
-            constexpr int st = decltype(ST)::value, u = st >> 2, v = st & 3, j = decltype(J)::value;
-            return lds_read_f4<buf * TB + (16 * u + 4 * v) * ROW * 4 + 256 * j>(va);
-        };
-        f32x4 vb[4];   // step 0's chunks load while the softmax runs
-        sfor<4>([&](auto J) { vb[decltype(J)::value] = vread(std::integral_constant<int, 0>{}, J); });
-        // Online softmax. s[u][v] is the score of key kb + 16u + 4v + g for query row r16.
-        float x[2][4], mx = -INFINITY;
-#pragma unroll
-        for (int u = 0; u < 2; u++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int key = kb + 16 * u + 4 * v + g;
-                const bool ok = q_valid && key < k_len && (!p.causal || key <= qpos);
-                x[u][v] = ok ? s[u][v] * p.scale : -INFINITY;
-                mx = fmaxf(mx, x[u][v]);
-            }
-        const float mn = fmaxf(m_run, xrow_max(mx));
-        float pv[2][4];
-        float alpha = 1.f, rs = 0.f;
-        if (mn != -INFINITY) {
-            alpha = (m_run == -INFINITY) ? 0.f : expf(m_run - mn);
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    pv[u][v] = x[u][v] == -INFINITY ? 0.f : expf(x[u][v] - mn);
-                    rs += pv[u][v];
-                }
-        } else {
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) pv[u][v] = 0.f;
-        }
-        m_run = mn;
-        l_run = l_run * alpha + rs;
-        const float alpha_o = alpha;
-        // O^T += V^T . P^T: 8 four-key steps (u, v), each 16 dim tiles. The V chunks roll
-        // through four registers: chunk j of the next step is read as soon as the current
-        // step's chunk j has fed its four products, so three reads are always in flight.
-#pragma unroll
-        for (int n = 0; n < 16; n++) o[n] *= alpha_o;
-        sfor<8>([&](auto S) {
-            constexpr int st = decltype(S)::value, u = st >> 2, v = st & 3;
-            const float b = pv[u][v];
-            sfor<4>([&](auto J) {
-                constexpr int j = decltype(J)::value;
-                if constexpr (st + 1 < 8) lds_wait_f4<3>(vb[j]);
-                else lds_wait_f4<3 - j>(vb[j]);
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    o[4 * j + e] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb[j][e], b, o[4 * j + e], 0, 0, 0);
-                if constexpr (st + 1 < 8) vb[j] = vread(std::integral_constant<int, st + 1>{}, J);
-            });
-        });
         __builtin_amdgcn_s_waitcnt(0);
-        if (ti + 1 < n_tiles) clear_tail(kb + BK, smem + 2 * TILE + (buf ^ 1) * TILE);
+        if (n_tiles > 0) clear_tail(cur, 0, smem + 2 * TILE);
         __syncthreads();
-    };
-    for (int ti = 0; ti < n_tiles; ti += 2) {
-        tile(ti, std::integral_constant<int, 0>{});
-        if (ti + 1 < n_tiles) tile(ti + 1, std::integral_constant<int, 1>{});
-    }
 
-    // ---- epilogue: O = O^T / l, times sigmoid(gate). Accumulator n = 4j + e, entry v of lane
-    // (g, r16) is dim 64j + 16g + 4v + e of row r16.
-    float l_row = l_run;
-    l_row += __shfl_xor(l_row, 16);
-    l_row += __shfl_xor(l_row, 32);
-    if (q_valid) {
-        const float il = l_row > 0.f ? 1.0f / l_row : 0.f;
-        const float *grow = p.qkv + (size_t)t * p.row + (size_t)h * 2 * HD + HD;
-        const size_t obase = (size_t)t * p.nh * HD + (size_t)h * HD;
+        f32x4 o[16];
 #pragma unroll
-        for (int v = 0; v < 4; v++)
+        for (int n = 0; n < 16; n++) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float m_run = -INFINITY, l_run = 0.f;
+
+        auto tile = [&](const int ti, auto BUF) {
+            constexpr int buf = decltype(BUF)::value;
+            const int kb = ti * BK;
+            if (ti + 1 < n_tiles) fill(cur, kb + BK, smem + (buf ^ 1) * TILE, smem + 2 * TILE + (buf ^ 1) * TILE);
+            if (cur.live) {   // wave-uniform: a spare wave of the last head chunk only fills
+                // S^T: two 16-key subtiles, 64 four-dim steps each, their products interleaved
+                // (two independent accumulator chains); K read in runs of RUN chunks per subtile
+                f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+                sfor<NRUN>([&](auto H) {
+                    constexpr int hh = decltype(H)::value;
+                    f32x4 a[2][RUN];
+                    sfor<RUN>([&](auto J) {
+                        constexpr int j = decltype(J)::value;
+                        a[0][j] = lds_read_f4<buf * TB + (RUN * hh + j) * 16>(ka);
+                        a[1][j] = lds_read_f4<buf * TB + 16 * ROW * 4 + (RUN * hh + j) * 16>(ka);
+                    });
+                    sfor<RUN>([&](auto J) {
+                        constexpr int j = decltype(J)::value;
+                        lds_wait_f4<2 * (RUN - 1 - j) + 1>(a[0][j]);
+                        lds_wait_f4<2 * (RUN - 1 - j)>(a[1][j]);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int d = 64 * j + 16 * g + 4 * v;
-                f32x4 w;
+                        for (int e = 0; e < 4; e++) {
+                            s[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0][j][e], qf[4 * (RUN * hh + j) + e], s[0], 0, 0, 0);
+                            s[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1][j][e], qf[4 * (RUN * hh + j) + e], s[1], 0, 0, 0);
+                        }
+                    });
+                });
+                // V chunk j of step st = (u, v): key 16u + 4v + g, chunk 16j + r16 of its row
+                auto vread = [&](auto ST, auto J) {
+                    constexpr int st = decltype(ST)::value, u = st >> 2, v = st & 3, j = decltype(J)::value;
+                    return lds_read_f4<buf * TB + (16 * u + 4 * v) * ROW * 4 + 256 * j>(va);
+                };
+                f32x4 vb[4];   // step 0's chunks load while the softmax runs
+                sfor<4>([&](auto J) { vb[decltype(J)::value] = vread(std::integral_constant<int, 0>{}, J); });
+                // Online softmax. s[u][v] is the score of key kb + 16u + 4v + g for query row r16.
+                float x[2][4], mx = -INFINITY;
 #pragma unroll
-                for (int e = 0; e < 4; e++) w[e] = o[4 * j + e][v] * il;
-                if (p.gate) {
-                    const f32x4 gv = *(const f32x4 *)(grow + d);
+                for (int u = 0; u < 2; u++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) w[e] = w[e] * (1.0f / (1.0f + expf(-gv[e])));
+                    for (int v = 0; v < 4; v++) {
+                        const int key = kb + 16 * u + 4 * v + g;
+                        const bool ok = q_valid && key < k_len && (!p.causal || key <= qpos);
+                        x[u][v] = ok ? s[u][v] * p.scale : -INFINITY;
+                        mx = fmaxf(mx, x[u][v]);
+                    }
+                const float mn = fmaxf(m_run, xrow_max(mx));
+                float pv[2][4];
+                float alpha = 1.f, rs = 0.f;
+                if (mn != -INFINITY) {
+                    alpha = (m_run == -INFINITY) ? 0.f : expf(m_run - mn);
+#pragma unroll
+                    for (int u = 0; u < 2; u++)
+#pragma unroll
+                        for (int v = 0; v < 4; v++) {
+                            pv[u][v] = x[u][v] == -INFINITY ? 0.f : expf(x[u][v] - mn);
+                            rs += pv[u][v];
+                        }
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 2; u++)
+#pragma unroll
+                        for (int v = 0; v < 4; v++) pv[u][v] = 0.f;
                 }
-                store_out4(p.out, obase + d, w, p.out_type, p.f16_lim, flag);
+                m_run = mn;
+                l_run = l_run * alpha + rs;
+                const float alpha_o = alpha;
+                // O^T += V^T . P^T: 8 four-key steps (u, v), each 16 dim tiles. The V chunks roll
+                // through four registers: chunk j of the next step is read as soon as the current
+                // step's chunk j has fed its four products, so three reads are always in flight.
+#pragma unroll
+                for (int n = 0; n < 16; n++) o[n] *= alpha_o;
+                sfor<8>([&](auto S) {
+                    constexpr int st = decltype(S)::value, u = st >> 2, v = st & 3;
+                    const float b = pv[u][v];
+                    sfor<4>([&](auto J) {
+                        constexpr int j = decltype(J)::value;
+                        if constexpr (st + 1 < 8) lds_wait_f4<3>(vb[j]);
+                        else lds_wait_f4<3 - j>(vb[j]);
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            o[4 * j + e] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb[j][e], b, o[4 * j + e], 0, 0, 0);
+                        if constexpr (st + 1 < 8) vb[j] = vread(std::integral_constant<int, st + 1>{}, J);
+                    });
+                });
             }
+            __builtin_amdgcn_s_waitcnt(0);
+            if (ti + 1 < n_tiles) clear_tail(cur, kb + BK, smem + 2 * TILE + (buf ^ 1) * TILE);
+            __syncthreads();
+        };
+        for (int ti = 0; ti < n_tiles; ti += 2) {
+            tile(ti, std::integral_constant<int, 0>{});
+            if (ti + 1 < n_tiles) tile(ti + 1, std::integral_constant<int, 1>{});
+        }
+
+        // ---- the next item's first tile loads into the buffers the key loop has left (every
+        // wave passed its closing barrier) while this item's epilogue runs
+        const Item done = cur;
+        k++;
+        const bool more = advance(k, cur);
+        if (more && cur.n_tiles > 0) fill(cur, 0, smem, smem + 2 * TILE);
+
+        // ---- epilogue: O = O^T / l, times sigmoid(gate). Accumulator n = 4j + e, entry v of lane
+        // (g, r16) is dim 64j + 16g + 4v + e of row r16.
+        float l_row = l_run;
+        l_row += __shfl_xor(l_row, 16);
+        l_row += __shfl_xor(l_row, 32);
+        if (q_valid && done.live) {
+            const float il = l_row > 0.f ? 1.0f / l_row : 0.f;
+            const float *grow = p.qkv + (size_t)t * p.row + (size_t)h * 2 * HD + HD;
+            const size_t obase = (size_t)t * p.nh * HD + (size_t)h * HD;
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int d = 64 * j + 16 * g + 4 * v;
+                    f32x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) w[e] = o[4 * j + e][v] * il;
+                    if (p.gate) {
+                        const f32x4 gv = *(const f32x4 *)(grow + d);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) w[e] = w[e] * (1.0f / (1.0f + expf(-gv[e])));
+                    }
+                    store_out4(p.out, obase + d, w, p.out_type, p.f16_lim, done.flag);
+                }
+        }
+        if (!more) break;
     }
 }
 

@@ -145,9 +145,10 @@ typedef struct {
                                  CLEF_HIP_QKV_F32 (1): the FP32 path (clef_metal.m:1330-1413,
                                  attn_prep + attention_prefetch_64 and kin): f32 rows, f32 K and V
                                  planes, FP32 products and softmax, for the per-record rerun after
-                                 an overflow (clef.c:526-550) and CLEF_ATTN_TU=0. In FP32 mode nh /
-                                 nkv must be at most 8, sched and trace are ignored, and only the
-                                 output (f16 out_type) can flag. Other values are rejected */
+                                 an overflow (clef.c:526-550) and CLEF_ATTN_TU=0. In FP32 mode any
+                                 nh / nkv works (groups above 8 heads run as several head
+                                 chunks), sched and trace are ignored, and only the output (f16
+                                 out_type) can flag. Other values are rejected */
     const int32_t *tok_kv;    /* [T] device int32: the plan's pass row -> plane row map (the inverse
                                  of kv_tok); the bf16 K/V prologue runs over pass rows with it */
 } clef_hip_attn_args;

@@ -146,7 +146,23 @@ def test_fp32_prefix_equals_full_pass_bitwise():
     assert torch.equal(part.view(torch.int32), full[a:].view(torch.int32))
 
 
-def test_fp32_rejects_wide_groups():
-    w = _fp32(dict(workloads.text_inputs([40], 9, 1, seed=1), gate=True, theta=1e7))
-    with pytest.raises(RuntimeError, match="at most 8"):
-        _run(w)
+@pytest.mark.parametrize("nh,nkv", [(12, 1), (16, 1), (9, 1), (24, 2)])
+def test_fp32_wide_groups(nh, nkv):
+    """Groups of more than 8 q heads (12 and 16 per kv head; 9, whose second chunk has a spare
+    wave; 12 per kv head over two kv heads) run as head chunks, against float64 within the FP32
+    bound, with ragged records."""
+    _say(f"[fp32] wide group {nh}/{nkv}")
+    w = _fp32(dict(workloads.text_inputs([1, 17, 40, 130, 300], nh, nkv, seed=nh), gate=True, theta=1e7))
+    out, _ = _run(w)
+    _check_fp32(out.cpu().numpy(), w, what=f"{nh}/{nkv}")
+
+
+def test_fp32_persistent_grid_matches_one_item_per_workgroup(monkeypatch):
+    """The persistent grid (CLEF_HIP_F32_PERSISTENT=1: items in snake order, the next item's
+    first tile loading during the epilogue) gives bitwise the output of one workgroup per item."""
+    _say("[fp32] persistent grid vs one item per workgroup")
+    w = _fp32(dict(workloads.text_inputs([700, 33, 129, 1, 260], 24, 4, seed=3), gate=True, theta=1e7))
+    one, _ = _run(w)
+    monkeypatch.setenv("CLEF_HIP_F32_PERSISTENT", "1")
+    out, _ = _run(w)
+    assert torch.equal(out.view(torch.int32), one.view(torch.int32))
