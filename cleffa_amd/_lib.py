@@ -71,6 +71,7 @@ class VisArgs(ctypes.Structure):
         ("q_plane", c_void_p), ("k_plane", c_void_p), ("vt_plane", c_void_p), ("kvT", c_int),
         ("blocks", c_void_p), ("n_blk", c_int), ("kv_tok", c_void_p), ("kv_rows", c_int),
         ("out", c_void_p), ("out_type", c_int), ("f16_lim", c_float), ("ovf", c_void_p),
+        ("tok_kv", c_void_p),
     ]
 
 

@@ -351,9 +351,11 @@ class VisionAttention:
         self.inv_freq = torch.from_numpy(rope_inv_freq(theta, hd // 2).copy()).to(self.device)
 
     def forward(self, qkv, bias, pos2, plan, out=None, out_dtype="bf16", ovf=None,
-                f16_lim=65504.0, stream=None, scratch=None, noalloc=False):
+                f16_lim=65504.0, stream=None, scratch=None, noalloc=False, rows_prologue=True):
         """noalloc: run clef_hip_vis_attention_noalloc, whose planes are the library's own
-        device scratch (no plane tensors are made; `out` is still allocated here if None)."""
+        device scratch (no plane tensors are made; `out` is still allocated here if None).
+        rows_prologue: hand the library the plan's tok_kv, so the prologue runs over patches
+        (else it runs over plane rows through kv_tok)."""
         lib = _lib.load()
         if plan.causal or plan.cu_k is not None:
             raise ValueError("vision attention takes a bidirectional fresh plan")
@@ -384,6 +386,7 @@ class VisionAttention:
         a.q_plane, a.k_plane, a.vt_plane, a.kvT = _ptr(q_plane), _ptr(k_plane), _ptr(vt_plane), kvT
         a.blocks, a.n_blk, a.kv_tok, a.kv_rows = _ptr(plan.blocks), plan.n_blk, _ptr(plan.kv_tok), plan.kv_rows
         a.out, a.out_type, a.f16_lim, a.ovf = _ptr(out), out_type, f16_lim, _ptr(ovf)
+        a.tok_kv = _ptr(plan.tok_kv) if rows_prologue else None
         err = _err()
         fn = lib.clef_hip_vis_attention_noalloc if noalloc else lib.clef_hip_vis_attention
         _lib.check(fn(ctypes.byref(a), _stream_handle(stream), err, len(err)), err)

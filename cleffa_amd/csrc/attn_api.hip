@@ -164,8 +164,12 @@ bool vis_run(const clef_hip_vis_args *a, uint16_t *q_plane, uint16_t *k_plane, u
         VisPrepParams q;
         q.qkv = a->qkv; q.bias = a->bias; q.pos2 = a->pos2; q.inv_freq = a->inv_freq; q.kv_tok = a->kv_tok;
         q.q_plane = q_plane; q.k_plane = k_plane; q.vt_plane = vt_plane;
-        q.P = a->P; q.heads = a->heads; q.kvT = a->kvT; q.kv_rows = a->kv_rows;
-        hipLaunchKernelGGL(vis_prep_kernel, dim3(((a->kv_rows + 15) / 16 * a->heads + 31) / 32 * 32), dim3(256), 0, (hipStream_t)stream, q);
+        q.P = a->P; q.heads = a->heads; q.kvT = a->kvT; q.kv_rows = a->kv_rows; q.tok_kv = a->tok_kv;
+        if (a->tok_kv)
+            hipLaunchKernelGGL(vis_prep_rows_kernel, dim3((a->P + kVisRowsBM - 1) / kVisRowsBM, (a->heads + kVisRowsHeads - 1) / kVisRowsHeads + a->heads),
+                               dim3(kVisRowsThreads), 0, (hipStream_t)stream, q);
+        else
+            hipLaunchKernelGGL(vis_prep_kernel, dim3(((a->kv_rows + 15) / 16 * a->heads + 31) / 32 * 32), dim3(256), 0, (hipStream_t)stream, q);
         if (!launch_ok("vis_prep", err, errlen)) return false;
     }
     if (a->n_blk == 0) return true;

@@ -153,6 +153,110 @@ __device__ __forceinline__ float row16_sum(float v) {   // sum over the lane's 1
 // 256 threads: 16 lanes per row for the loads and stores, one lane per (row, pair) for the
 // rotary, the rows staged in LDS.
 // ------------------------------------------------------------------------------------------
+// The vision prologue over pass rows (the form used when the caller passes tok_kv): workgroup
+// (b, g) takes patches 64b .. 64b + 63: for g < G (the groups of 8 heads) the q and k of heads
+// 8g .. 8g + 7, for g >= G the v of head g - G (workgroups of their own, so the two run side by
+// side). Everything goes through registers, with no LDS tile and no plane-row lookup ahead of the
+// loads. The rows' rotary cos/sin go to an LDS table while the q/k loads land (the angles do not
+// depend on the head: eight heads share it).
+//  - q and k: thread (dims 4j .. 4j + 3, head) holds both halves of four rotary pairs (dims
+//    4j + e and 4j + 36 + e) for 8 rows, loaded as 8-byte pieces, biased and turned in
+//    registers, stored to the Q plane (row = patch) and the K plane (row = tok_kv);
+//  - v (workgroups of one head, one wave per 16-byte chunk of 8 dims): lane = row, biased, then
+//    stored dim by dim: each store covers 64 consecutive plane rows of an image, one 128-byte
+//    V^T line.
+// Same arithmetic as vis_prep_kernel (metal/clef.metal:1616-1656: bias in f32, pair (i, i + 36)
+// turned by the grid row's angle for i < 18 and the column's otherwise, each result rounded once
+// to bf16).
+constexpr int kVisRowsBM = 64, kVisRowsHeads = 8, kVisRowsThreads = 576;
+__global__ __launch_bounds__(kVisRowsThreads) void vis_prep_rows_kernel(VisPrepParams p) {
+    constexpr int HD = 72, HALF = HD / 2, QUART = HD / 4, CH = HD / 8, BM = kVisRowsBM, HG = kVisRowsHeads;
+    constexpr int NT = kVisRowsThreads, RPT = 8;   // q/k: (HALF / 4) x HG x (BM / RPT) threads, RPT rows each
+    static_assert((HALF / 4) * HG * (BM / RPT) == NT, "q/k threads");
+    __shared__ float2 table[BM * HALF];   // [row][pair] (cos, sin)
+    const int tid = threadIdx.x, m0 = blockIdx.x * BM;
+    const int n_groups = (p.heads + HG - 1) / HG;
+    const bool is_v = (int)blockIdx.y >= n_groups;
+    const int E = p.heads * HD;
+    if (is_v) {
+        // v: head blockIdx.y - G, wave c takes dims 8c .. 8c + 7 of the 64 rows; lane = row
+        static_assert(NT / 64 == CH, "one wave per 16-byte chunk of a v row");
+        const int lane = tid & 63, c = tid >> 6, t = min(m0 + lane, p.P - 1), h = blockIdx.y - n_groups;
+        const u32x4 v = *(const u32x4 *)(p.qkv + (size_t)t * 3 * E + 2 * (size_t)E + (size_t)h * HD + 8 * c);
+        float bb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (p.bias) {
+            const float *bp = p.bias + 2 * (size_t)E + (size_t)h * HD + 8 * c;
+            const float4 b0 = *(const float4 *)bp, b1 = *(const float4 *)(bp + 4);
+            bb[0] = b0.x; bb[1] = b0.y; bb[2] = b0.z; bb[3] = b0.w; bb[4] = b1.x; bb[5] = b1.y; bb[6] = b1.z; bb[7] = b1.w;
+        }
+        if (m0 + lane >= p.P) return;
+        uint16_t *col = p.vt_plane + ((size_t)h * HD + 8 * c) * p.kvT + (size_t)p.tok_kv[t];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            col[(size_t)(2 * e) * p.kvT] = f2bf(bf_lo(v[e]) + bb[2 * e]);
+            col[(size_t)(2 * e + 1) * p.kvT] = f2bf(bf_hi(v[e]) + bb[2 * e + 1]);
+        }
+        return;
+    }
+    const int h0 = blockIdx.y * HG, hg = min(HG, p.heads - h0);
+    // q and k: the loads go out first, the cos/sin table is computed while they land
+    const int j = tid % (HALF / 4), hh = (tid / (HALF / 4)) % HG, rg = tid / (HALF / 4 * HG);
+    const int h = h0 + min(hh, hg - 1);
+    uint2 x[RPT][2][2];
+#pragma unroll
+    for (int k = 0; k < RPT; k++) {
+        const int t = min(m0 + rg * RPT + k, p.P - 1);
+        const uint16_t *row = p.qkv + (size_t)t * 3 * E + (size_t)h * HD + 4 * j;
+#pragma unroll
+        for (int part = 0; part < 2; part++)
+#pragma unroll
+            for (int s = 0; s < 2; s++) x[k][part][s] = *(const uint2 *)(row + (size_t)part * E + s * HALF);
+    }
+    float b[2][2][4];   // [q, k][dims 4j.., 4j + 36..][e]
+#pragma unroll
+    for (int part = 0; part < 2; part++)
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (p.bias) v = *(const float4 *)(p.bias + (size_t)part * E + (size_t)h * HD + 4 * j + s * HALF);
+            b[part][s][0] = v.x; b[part][s][1] = v.y; b[part][s][2] = v.z; b[part][s][3] = v.w;
+        }
+    for (int id = tid; id < BM * HALF; id += NT) {
+        const int r = id / HALF, i = id % HALF, t = min(m0 + r, p.P - 1);
+        const float pos = (float)p.pos2[2 * (size_t)t + (i < QUART ? 0 : 1)];
+        float sn, cs;
+        rope_sincos(pos * p.inv_freq[i < QUART ? i : i - QUART], &sn, &cs);
+        table[id] = make_float2(cs, sn);
+    }
+    __syncthreads();
+    if (hh >= hg) return;
+#pragma unroll
+    for (int k = 0; k < RPT; k++) {
+        const int r = rg * RPT + k, t = m0 + r;
+        if (t >= p.P) break;
+        const float2 *c = table + r * HALF + 4 * j;
+        const float2 c4[4] = {c[0], c[1], c[2], c[3]};
+        const size_t kv = (size_t)p.tok_kv[t];
+#pragma unroll
+        for (int part = 0; part < 2; part++) {
+            const uint2 lo = x[k][part][0], hi = x[k][part][1];
+            const float a[4] = {bf_lo(lo.x) + b[part][0][0], bf_hi(lo.x) + b[part][0][1], bf_lo(lo.y) + b[part][0][2], bf_hi(lo.y) + b[part][0][3]};
+            const float z[4] = {bf_lo(hi.x) + b[part][1][0], bf_hi(hi.x) + b[part][1][1], bf_lo(hi.y) + b[part][1][2], bf_hi(hi.y) + b[part][1][3]};
+            uint16_t ro[4], rh[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                ro[e] = f2bf(fmaf(a[e], c4[e].x, -z[e] * c4[e].y));
+                rh[e] = f2bf(fmaf(z[e], c4[e].x, a[e] * c4[e].y));
+            }
+            const uint2 wo = make_uint2(ro[0] | ((unsigned)ro[1] << 16), ro[2] | ((unsigned)ro[3] << 16));
+            const uint2 wh = make_uint2(rh[0] | ((unsigned)rh[1] << 16), rh[2] | ((unsigned)rh[3] << 16));
+            uint16_t *dst = part == 0 ? p.q_plane + ((size_t)h * p.P + t) * HD : p.k_plane + ((size_t)h * p.kvT + kv) * HD;
+            *(uint2 *)(dst + 4 * j) = wo;
+            *(uint2 *)(dst + 4 * j + HALF) = wh;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void vis_prep_kernel(VisPrepParams p) {
     constexpr int HD = 72, ROWS = 16, HALF = HD / 2, QUART = HD / 4, CH = HD / 8;   // 9 chunks
     constexpr int VS = ROWS + 8;   // LDS stride of a V^T row
@@ -232,10 +336,11 @@ __global__ __launch_bounds__(256) void vis_prep_kernel(VisPrepParams p) {
         rope_sincos(ang_pos[row][i < QUART ? 0 : 1] * fr[r], &sn, &cs);
         const float q0 = xs[row][0][i], q1 = xs[row][0][i + HALF];
         const float k0 = xs[row][1][i], k1 = xs[row][1][i + HALF];
-        qo[row][i] = f2bf(q0 * cs - q1 * sn);
-        qo[row][i + HALF] = f2bf(q1 * cs + q0 * sn);
-        ko[row][i] = f2bf(k0 * cs - k1 * sn);
-        ko[row][i + HALF] = f2bf(k1 * cs + k0 * sn);
+        // explicit fmas: the rounding is the same in every form of the prologue
+        qo[row][i] = f2bf(fmaf(q0, cs, -q1 * sn));
+        qo[row][i + HALF] = f2bf(fmaf(q1, cs, q0 * sn));
+        ko[row][i] = f2bf(fmaf(k0, cs, -k1 * sn));
+        ko[row][i + HALF] = f2bf(fmaf(k1, cs, k0 * sn));
     }
     for (int id = tid; id < ROWS * HD; id += 256) {
         const int row = id / HD, d = id % HD;

@@ -33,6 +33,7 @@ struct VisPrepParams {
     const int32_t *pos2;
     const float *inv_freq;
     const int32_t *kv_tok;    // patch of each plane row, -1: not written
+    const int32_t *tok_kv;    // plane row of each patch (the rows kernel)
     uint16_t *q_plane;
     uint16_t *k_plane;
     uint16_t *vt_plane;

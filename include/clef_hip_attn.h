@@ -222,6 +222,9 @@ typedef struct {
     int out_type;
     float f16_lim;
     int32_t *ovf;             /* [P] or NULL; flag at the image's first patch */
+    const int32_t *tok_kv;    /* [P] device int32 or NULL: the plan's patch -> plane row map (the
+                                 inverse of kv_tok); given, the prologue runs over patches with all
+                                 its loads at once, else over plane rows through kv_tok */
 } clef_hip_vis_args;
 
 bool clef_hip_vis_attention(const clef_hip_vis_args *a, void *stream, char *err, size_t errlen);

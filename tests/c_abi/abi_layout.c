@@ -29,7 +29,7 @@ int main(void) {
     F(clef_hip_vis_args, k_plane); F(clef_hip_vis_args, vt_plane); F(clef_hip_vis_args, kvT);
     F(clef_hip_vis_args, blocks); F(clef_hip_vis_args, n_blk); F(clef_hip_vis_args, kv_tok);
     F(clef_hip_vis_args, kv_rows); F(clef_hip_vis_args, out); F(clef_hip_vis_args, out_type);
-    F(clef_hip_vis_args, f16_lim); F(clef_hip_vis_args, ovf);
+    F(clef_hip_vis_args, f16_lim); F(clef_hip_vis_args, ovf); F(clef_hip_vis_args, tok_kv);
     Z(clef_hip_vis_args);
 
     F(clef_hip_omni_prep_args, nh); F(clef_hip_omni_prep_args, nkv); F(clef_hip_omni_prep_args, T);

@@ -231,6 +231,32 @@ def _vision_case(seed=3, grids=((4, 6), (16, 18), (2, 2), (6, 10)), heads=4):
     return VisionAttention(heads, hd), AttnPlan(cu, causal=False), qkv, pos2, cu
 
 
+def test_vision_prologue_forms_agree():
+    """The prologue over patches (tok_kv given) and over plane rows (kv_tok) write the same Q
+    plane, the same owned K and V^T plane rows and the same output, bit for bit, with the qkv
+    bias, over images of 4 to 288 patches (64-row tiles that cross images and end mid-tile)."""
+    _say("[vision] prologue over patches = over plane rows")
+    vis, plan, qkv, pos2, _ = _vision_case(seed=11, grids=((4, 6), (16, 18), (2, 2), (6, 10), (1, 4)), heads=6)
+    E = vis.E
+    gen = torch.Generator().manual_seed(12)
+    bias = (0.5 * torch.randn(3 * E, generator=gen)).cuda()
+    qkv = qkv.cuda()
+    res = []
+    for rows in (True, False):
+        scratch = vis.scratch(plan.T, plan.kvT)
+        for s in scratch:
+            s.zero_()
+        out = vis.forward(qkv, bias, pos2, plan, scratch=scratch, rows_prologue=rows)
+        torch.cuda.synchronize()
+        res.append((out, scratch))
+    (o1, (q1, k1, v1)), (o0, (q0, k0, v0)) = res
+    own = torch.from_numpy(np.flatnonzero(plan.kv_tok_host >= 0)).cuda()
+    assert torch.equal(_bits(q1), _bits(q0))
+    assert torch.equal(_bits(k1[:, own]), _bits(k0[:, own]))
+    assert torch.equal(_bits(v1[:, :, own]), _bits(v0[:, :, own]))
+    assert torch.equal(_bits(o1), _bits(o0))
+
+
 def test_vision_row_sums_with_unit_values():
     """V = 1: the output is the row sum of P over the row sum the ones row accumulated, exactly 1
     in f32, across images of 24 to 288 patches (tail tiles included)."""
