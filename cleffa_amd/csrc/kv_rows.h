@@ -29,12 +29,31 @@ struct KvRows {
     float *rope_cs;           // [T][n_rot / 2][2] or NULL
 };
 
+// The rotary cos/sin of row `row` (pass row m0 + row), pairs 2k and 2k + 1, into the table (and,
+// for kv head 0, into rope_cs for the Q prologue).
+__device__ __forceinline__ void k_table(const KvRows &p, int m0, int row, int k, int kh, float2 *table) {
+    const int t = m0 + row, half_rot = p.n_rot / 2;
+    if (t >= p.T) return;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int i = 2 * k + h;
+        const float ang = (float)p.pos3[3 * (size_t)t + i % 3] * p.inv_freq[i];
+        float sn, cn;
+        rope_sincos(ang, &sn, &cn);
+        table[32 * row + i] = make_float2(cn, sn);
+        if (p.rope_cs && kh == 0) *(float2 *)(p.rope_cs + (size_t)t * 2 * half_rot + 2 * i) = make_float2(cn, sn);
+    }
+}
+
 // K rows m0 .. m0 + BM - 1 of kv head kh (those below T): 16 lanes per row, 16 dims per lane,
 // NTHREADS / 16 rows per pass. Each pass first computes the rotary cos/sin of its rows, two
 // pairs per lane, into `table` (LDS, [NTHREADS / 16][32] float2), and kv head 0 stores them in
 // rope_cs for the Q prologue. Every thread runs every pass (the table needs two barriers).
-template <int NTHREADS, int BM>
+// TABLED: one pass (NTHREADS / 16 == BM) whose table the caller has already filled with k_table
+// and made visible.
+template <int NTHREADS, int BM, bool TABLED = false>
 __device__ __forceinline__ void k_rows(const KvRows &p, const uint8_t *ct, int cs, int m0, int kh, float2 *table) {
+    static_assert(!TABLED || NTHREADS / 16 == BM, "a caller-filled table covers one pass");
     constexpr int HD = 256, RPP = NTHREADS / 16;
     const int tid = threadIdx.x, rr = tid >> 4, k = tid & 15;
     const int half_rot = p.n_rot / 2;   // 0 or 32: dims [0, 32) pair with [32, 64)
@@ -49,18 +68,8 @@ __device__ __forceinline__ void k_rows(const KvRows &p, const uint8_t *ct, int c
     for (int pass = 0; pass < BM / RPP; pass++) {
         const int row = RPP * pass + rr, t = m0 + row;
         const bool valid = t < p.T;
-        if (half_rot) {
-            if (valid) {
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int i = 2 * k + h;
-                    const float ang = (float)p.pos3[3 * (size_t)t + i % 3] * p.inv_freq[i];
-                    float sn, cn;
-                    rope_sincos(ang, &sn, &cn);
-                    table[32 * rr + i] = make_float2(cn, sn);
-                    if (p.rope_cs && kh == 0) *(float2 *)(p.rope_cs + (size_t)t * 2 * half_rot + 2 * i) = make_float2(cn, sn);
-                }
-            }
+        if (half_rot && !TABLED) {
+            k_table(p, m0 + RPP * pass, rr, k, kh, table);
             __syncthreads();
         }
         if (valid) {
@@ -118,7 +127,7 @@ __device__ __forceinline__ void k_rows(const KvRows &p, const uint8_t *ct, int c
                 *(u32x4 *)(dst + 8 * h) = ko;
             }
         }
-        if (half_rot) __syncthreads();   // the table is read before the next pass rewrites it
+        if (half_rot && !TABLED) __syncthreads();   // the table is read before the next pass rewrites it
     }
 }
 
@@ -155,8 +164,9 @@ __device__ __forceinline__ void v_rows(const KvRows &p, const uint8_t *ct, int c
 
 // The K/V prologue as its own kernel, over pass rows: workgroup (b, j) loads rows 64b .. 64b + 63
 // of K head j (j < nkv) or V head j - nkv into LDS and runs k_rows / v_rows on them. All loads
-// are issued at once (no load depends on another), and the plane rows come from tok_kv.
-constexpr int kPrepRowsBM = 64, kPrepRowsThreads = 512, kPrepRowsCS = 512 + 16;
+// are issued at once (no load depends on another), a K workgroup fills its rotary table while
+// they land, and the plane rows come from tok_kv.
+constexpr int kPrepRowsBM = 64, kPrepRowsThreads = 1024, kPrepRowsCS = 512 + 16;
 __global__ __launch_bounds__(kPrepRowsThreads) void text_prep_rows_kernel(const uint16_t *qkv, int row_len, KvRows p) {
     constexpr int BM = kPrepRowsBM, NT = kPrepRowsThreads, CSB = kPrepRowsCS;
     __shared__ __attribute__((aligned(16))) uint8_t tile[BM * CSB];
@@ -165,14 +175,22 @@ __global__ __launch_bounds__(kPrepRowsThreads) void text_prep_rows_kernel(const 
     const bool is_k = j < p.nkv;
     const int head = is_k ? j : j - p.nkv;
     const uint16_t *src = qkv + (size_t)p.nh * 2 * 256 + (size_t)(is_k ? 0 : p.nkv * 256) + (size_t)head * 256;
+    constexpr int PER = BM * 32 / NT;
+    u32x4 w[PER];
 #pragma unroll
-    for (int i = 0; i < BM * 32 / NT; i++) {
+    for (int i = 0; i < PER; i++) {
         const int id = tid + NT * i, r = id >> 5, c16 = id & 31;
         const int t = min(m0 + r, p.T - 1);
-        *(u32x4 *)(tile + r * CSB + 16 * c16) = *(const u32x4 *)(src + (size_t)t * row_len + 8 * c16);
+        w[i] = *(const u32x4 *)(src + (size_t)t * row_len + 8 * c16);
+    }
+    if (is_k && p.n_rot) k_table(p, m0, tid >> 4, tid & 15, head, table);
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int id = tid + NT * i, r = id >> 5, c16 = id & 31;
+        *(u32x4 *)(tile + r * CSB + 16 * c16) = w[i];
     }
     __syncthreads();
-    if (is_k) k_rows<NT, BM>(p, tile, CSB, m0, head, table);
+    if (is_k) k_rows<NT, BM, true>(p, tile, CSB, m0, head, table);
     else v_rows<NT / 64, BM>(p, tile, CSB, m0, head);
 }
 
