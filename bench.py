@@ -398,6 +398,10 @@ def main():
         print(f"profile pass done: copy of {CALIB_BYTES} bytes, 3 steps of {a.config}", flush=True)
         return
     graph = not a.no_graph
+    # An untimed pass of the same shape first: in a fresh process the first timed pass of a HIP
+    # graph ran 8-10% slower than every later one (C1: 87.9 us, then 78.3-80.4 us over the next
+    # 11 passes), whatever eager warm-up preceded it.
+    time_fn(step, a.steps, a.warmup, graph)
     ms, wall_ms = time_fn(step, a.steps, a.warmup, graph)
     layer = info.get("layer")
     layer_info = None
@@ -433,7 +437,14 @@ def main():
                    **({"lengths": info["lengths"]} if "lengths" in info else {})},
     }
     if core is not None:
-        core_ms, _ = time_fn(core, a.steps, a.warmup, graph)
+        # The kernel alone and inside the step: three interleaved rounds of the step, the kernel
+        # alone and the K/V prologue alone (each round K steps), medians, so that all three see
+        # the same clock; in-step = step - prologue.
+        rounds = {"step": [], "core": [], "prep": []}
+        for _ in range(3):
+            for k, f in (("step", step), ("core", core), ("prep", prep)):
+                rounds[k].append(time_fn(f, a.steps, a.warmup, graph)[0])
+        core_ms = statistics.median(rounds["core"])
         achieved = flops / (core_ms * 1e-3) / 1e12
         peak = PEAK_F32_MFMA if a.fp32 else PEAK_BF16_TFLOPS
         kname = f"attn_text_f32_kernel<{info['nh'] // w['nkv']}>" if a.fp32 else "attn_text_kernel<64>"
@@ -452,10 +463,10 @@ def main():
             res["roofline"].update({"mfma_stream_ceiling": round(ceil_tf, 1), "mfma_stream_clock_ghz": round(ceil_ghz, 3),
                                     "frac_of_stream_ceiling": round(achieved / ceil_tf, 4)})
         # the kernel as it runs inside the step: the step minus the K/V prologue kernel alone
-        prep_ms, _ = time_fn(prep, a.steps, a.warmup, graph)
-        in_step = ms - prep_ms
+        prep_ms = statistics.median(rounds["prep"])
+        in_step = statistics.median(rounds["step"]) - prep_ms
         ach = flops / (in_step * 1e-3) / 1e12
-        res["roofline"].update({"launch_ms_in_step": round(in_step, 5), "achieved_replay": res["roofline"]["achieved"],
+        res["roofline"].update({"launch_ms_in_step": round(in_step, 5), "step_ms_rounds": round(statistics.median(rounds["step"]), 5), "achieved_replay": res["roofline"]["achieved"],
                                 "frac_replay": res["roofline"]["frac"], "achieved": round(ach, 2),
                                 "frac": round(ach / peak, 4)})
         if "frac_of_stream_ceiling" in res["roofline"]:
