@@ -46,22 +46,28 @@ __device__ __forceinline__ void k_table(const KvRows &p, int m0, int row, int k,
 }
 
 // K rows m0 .. m0 + BM - 1 of kv head kh (those below T): 16 lanes per row, 16 dims per lane,
-// NTHREADS / 16 rows per pass. Each pass first computes the rotary cos/sin of its rows, two
-// pairs per lane, into `table` (LDS, [NTHREADS / 16][32] float2), and kv head 0 stores them in
-// rope_cs for the Q prologue. Every thread runs every pass (the table needs two barriers).
-// TABLED: one pass (NTHREADS / 16 == BM) whose table the caller has already filled with k_table
-// and made visible.
+// NTHREADS / 16 rows per pass. Lane k of a row holds dims d(k, e), e < 16: for k < 4 the rotary
+// pairs in place, dims 8k + e and 32 + 8k + e for e < 8 (pair i = 8k + e is x[e], x[e + 8]), and
+// for k >= 4 dims 64 + 16(k - 4) + e; so the rotation needs no lane exchange. Each pass first
+// computes the rotary cos/sin of its rows, two pairs per lane, into `table` (LDS,
+// [NTHREADS / 16][32] float2), and kv head 0 stores them in rope_cs for the Q prologue. Every
+// thread runs every pass (the table needs two barriers). TABLED: one pass (NTHREADS / 16 == BM)
+// whose table the caller has already filled with k_table and made visible.
+__device__ __forceinline__ int k_lane_dim(int k, int h) {   // first dim of the lane's half h (8 dims)
+    return k < 4 ? 8 * k + 32 * h : 64 + 16 * (k - 4) + 8 * h;
+}
 template <int NTHREADS, int BM, bool TABLED = false>
 __device__ __forceinline__ void k_rows(const KvRows &p, const uint8_t *ct, int cs, int m0, int kh, float2 *table) {
     static_assert(!TABLED || NTHREADS / 16 == BM, "a caller-filled table covers one pass");
     constexpr int HD = 256, RPP = NTHREADS / 16;
     const int tid = threadIdx.x, rr = tid >> 4, k = tid & 15;
     const int half_rot = p.n_rot / 2;   // 0 or 32: dims [0, 32) pair with [32, 64)
+    const int d0 = k_lane_dim(k, 0), d1 = k_lane_dim(k, 1);
     float wn[16];
     if (p.k_norm) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const float4 w4 = *(const float4 *)(p.k_norm + 16 * k + 4 * q);
+            const float4 w4 = *(const float4 *)(p.k_norm + ((q < 2) ? d0 : d1) + 4 * (q & 1));
             wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
         }
     }
@@ -73,7 +79,7 @@ __device__ __forceinline__ void k_rows(const KvRows &p, const uint8_t *ct, int c
             __syncthreads();
         }
         if (valid) {
-            const u32x4 kw0 = *(const u32x4 *)(ct + row * cs + 32 * k), kw1 = *(const u32x4 *)(ct + row * cs + 32 * k + 16);
+            const u32x4 kw0 = *(const u32x4 *)(ct + row * cs + 2 * d0), kw1 = *(const u32x4 *)(ct + row * cs + 2 * d1);
             float x[16];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -91,40 +97,39 @@ __device__ __forceinline__ void k_rows(const KvRows &p, const uint8_t *ct, int c
 #pragma unroll
                 for (int e = 0; e < 16; e++) x[e] *= inv * wn[e];
             }
-            if (half_rot) {
-                // lanes 0, 1 hold dims 0-31, lanes 2, 3 their partners 32-63 (two lanes apart)
-                float y[16];
+            if (half_rot && k < 4) {   // pair 8k + e: x[e] turns with x[e + 8]
+                const float4 *c = (const float4 *)(table + 32 * rr + 8 * k);
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const float up = __builtin_amdgcn_update_dpp(0.f, x[e], 0x12e, 0xf, 0xf, false);   // lane + 2
-                    const float dn = __builtin_amdgcn_update_dpp(0.f, x[e], 0x122, 0xf, 0xf, false);   // lane - 2
-                    y[e] = (k & 2) ? dn : up;
-                }
-                if (k < 4) {
-                    const bool first = k < 2;
-                    const float2 *c = table + 32 * rr + 16 * (k & 1);
+                for (int q = 0; q < 4; q++) {
+                    const float4 cs2 = c[q];   // (cos, sin) of pairs 8k + 2q, 8k + 2q + 1
 #pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const float2 v = c[e];
-                        x[e] = first ? x[e] * v.x - y[e] * v.y : x[e] * v.x + y[e] * v.y;
+                    for (int h = 0; h < 2; h++) {
+                        const int e = 2 * q + h;
+                        const float cn = h ? cs2.z : cs2.x, sn = h ? cs2.w : cs2.y;
+                        const float x0 = x[e], x1 = x[e + 8];
+                        x[e] = x0 * cn - x1 * sn;
+                        x[e + 8] = x1 * cn + x0 * sn;
                     }
                 }
             }
-            bool bad = false;
-            const unsigned lim = __float_as_uint(p.f16_lim);
+            // split16's saturation: the largest magnitude decides (NaN propagates through the
+            // maximum, and fails the compare); only a row holding one takes the elementwise pass
+            float amax = 0.f;
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const bool over = (__float_as_uint(x[e]) & 0x7fffffffu) > lim;
-                x[e] = over ? copysignf(65504.f, x[e]) : x[e];
-                bad |= over;
+            for (int e = 0; e < 16; e += 2)
+                amax = __builtin_elementwise_maximum(amax, __builtin_elementwise_maximum(fabsf(x[e]), fabsf(x[e + 1])));
+            if (!(amax <= p.f16_lim)) {
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    if (!(fabsf(x[e]) <= p.f16_lim)) x[e] = copysignf(65504.f, x[e]);
+                if (p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (bad && p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            uint16_t *dst = p.k_plane + ((size_t)kh * p.kvT + p.tok_kv[t]) * HD + 16 * k;
+            uint16_t *dst = p.k_plane + ((size_t)kh * p.kvT + p.tok_kv[t]) * HD;
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const float *xs = x + 8 * h;
                 u32x4 ko = {pack_f16(xs[0], xs[1]), pack_f16(xs[2], xs[3]), pack_f16(xs[4], xs[5]), pack_f16(xs[6], xs[7])};
-                *(u32x4 *)(dst + 8 * h) = ko;
+                *(u32x4 *)(dst + (h ? d1 : d0)) = ko;
             }
         }
         if (half_rot && !TABLED) __syncthreads();   // the table is read before the next pass rewrites it
