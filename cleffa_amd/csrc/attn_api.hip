@@ -184,11 +184,14 @@ bool vis_run(const clef_hip_vis_args *a, uint16_t *q_plane, uint16_t *k_plane, u
     return launch_ok("attn_vis", err, errlen);
 }
 
-// The FP32 core over the (16-row sub-block, kv head, head chunk) items, W waves per workgroup
-// (the kernel's 130 KB of LDS allow one workgroup per CU).
+// The FP32 core over the (16-row sub-block, kv head, head chunk) items (the kernel's LDS allows
+// one workgroup per CU): a chunk of W <= 6 heads runs two waves per head, each on half of the
+// head dims, so that the waves spread evenly over the four SIMDs (12 for the 6 q heads of a
+// 24 / 4 model); 7 and 8 heads run one wave per head.
 template <int W>
 void launch_f32(const text32::Params &p, long grid, hipStream_t s) {
-    hipLaunchKernelGGL(text32::attn_text_f32_kernel<W>, dim3((unsigned)grid), dim3(64 * W), 0, s, p);
+    constexpr int X = W <= 6 ? 2 : 1;
+    hipLaunchKernelGGL((text32::attn_text_f32_kernel<W, X>), dim3((unsigned)grid), dim3(64 * W * X), 0, s, p);
 }
 
 bool core_f32(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {

@@ -157,16 +157,28 @@ __device__ __forceinline__ void sfor(F &&f) {
 }
 
 // Work items are (16-row sub-block, kv head, head chunk): the kv group's G = nh / nkv q heads
-// split into n_chunks chunks of at most W <= 8 heads, one wave per head (a chunk's spare waves
-// fill tiles and take barriers but compute nothing). Items run in the plan's longest-first
+// split into n_chunks chunks of at most W <= 8 heads, X waves per head (a chunk's spare waves
+// fill tiles and take barriers but compute nothing). With X = 2 the two waves of a head split
+// its 256 dims: wave (slot s, half x), wave id s + W x, holds Q steps c = 4j + e of the chunks
+// j in {4x .. 4x + 3, 8 + 4x .. 8 + 4x + 3} (so a rotary pair (i, i + 32) stays in one wave)
+// and O for dims 128x .. 128x + 127; the halves' partial scores meet through LDS and each wave
+// adds its partner's to its own (the same sum in both, bitwise), then both run the softmax. Six
+// q heads then fill twelve waves, three per SIMD, where six waves left two SIMDs with one. Items run in the plan's longest-first
 // block order, each block's last 16 rows (its longest causal rows) first. With G workgroups,
 // workgroup b takes items b, then 2G - 1 - b, ... (snake order, so long and short items mix;
 // one item each when G is the item count); while an item's epilogue runs, the next item's
 // first K / V tile loads into the idle LDS buffers.
-template <int W>
-__global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
+template <int W, int X>
+__global__ __launch_bounds__(64 * W * X) void attn_text_f32_kernel(Params p) {
+    static_assert(X == 1 || X == 2, "one or two waves per head");
+    constexpr int NW = W * X;           // waves
+    constexpr int QN = 64 / X;          // Q steps (and B registers) per wave
     __shared__ __attribute__((aligned(16))) float smem[4 * TILE];   // K0 | K1 | V0 | V1
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // partial scores of the two halves: slot (wave, lane) holds its two 16-key subtiles
+    __shared__ __attribute__((aligned(16))) f32x4 xch[X > 1 ? NW * 64 * 2 : 1];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int slot = X == 1 ? wave : wave % W, half = X == 1 ? 0 : wave / W;   // head slot in the chunk, dim half
     const int r16 = lane & 15, g = lane >> 4;
     const int group = p.nh / p.nkv;
     const int n_items = p.n_blk * SUB * p.nkv * p.n_chunks;
@@ -193,7 +205,7 @@ __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
         it.k_len = p.causal ? min(blk[4], it.q_pos0 + it.nq) : blk[4];
         it.n_tiles = (it.k_len + BK - 1) / BK;
         it.flag = p.ovf ? p.ovf + blk[5] : nullptr;
-        const int hw = chunk * W + wave;
+        const int hw = chunk * W + slot;
         it.live = hw < group;
         it.h = it.kh * group + (it.live ? hw : 0);
         return true;
@@ -207,11 +219,11 @@ __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
         return false;
     };
 
-    // ---- tile fills: one 1 KB DMA group per key row; wave w fills rows w, w + W, ...
+    // ---- tile fills: one 1 KB DMA group per key row; wave w fills rows w, w + NW, ...
     auto fill = [&](const Item &it, int kb, float *Ks, float *Vs) {
         const float *kbase = p.k_plane + ((size_t)it.kh * p.kvT + it.k_row0) * HD;
         const float *vbase = p.v_plane + ((size_t)it.kh * p.kvT + it.k_row0) * HD;
-        for (int r = wave; r < BK; r += W) {
+        for (int r = wave; r < BK; r += NW) {
             const size_t off = (size_t)(kb + r) * HD + 4 * lane;
             __builtin_amdgcn_global_load_lds((const void *)(kbase + off), (lds_void *)(Ks + r * ROW), 16, 0, 0);
             __builtin_amdgcn_global_load_lds((const void *)(vbase + off), (lds_void *)(Vs + r * ROW), 16, 0, 0);
@@ -221,14 +233,17 @@ __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
     // zero probabilities of masked keys give exact zero products.
     auto clear_tail = [&](const Item &it, int kb, float *Vs) {
         if (kb + BK <= it.k_len) return;                  // workgroup-uniform
-        for (int r = wave; r < BK; r += W)
+        for (int r = wave; r < BK; r += NW)
             if (kb + r >= it.k_len) *(f32x4 *)(Vs + r * ROW + 4 * lane) = f32x4{0.f, 0.f, 0.f, 0.f};
     };
 
     const unsigned lds0 = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) float *)smem;
-    // K: row 4(r16 % 4) + r16 / 4 of subtile 0, chunk 16g; V: row g, chunk r16 (buffer 0)
-    const unsigned ka = lds0 + (unsigned)(4 * (r16 & 3) + (r16 >> 2)) * ROW * 4u + 256u * g;
-    const unsigned va = lds0 + 2u * TB + (unsigned)g * ROW * 4u + 16u * r16;
+    // K: row 4(r16 % 4) + r16 / 4 of subtile 0, chunk 16g (+ 4 half); V: row g, chunk r16
+    // (+ 32 half) (buffer 0)
+    const unsigned ka = lds0 + (unsigned)(4 * (r16 & 3) + (r16 >> 2)) * ROW * 4u + 256u * g + 64u * half;
+    const unsigned va = lds0 + 2u * TB + (unsigned)g * ROW * 4u + 16u * r16 + 512u * half;
+    // the K chunk (of 16 per 64 dims) of this wave's chunk step q4
+    auto kchunk = [](int q4) { return X == 1 ? q4 : (q4 < 4 ? q4 : q4 + 4); };
 
     int k = 0;
     Item cur;
@@ -241,43 +256,59 @@ __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
         const int h = cur.h;
         const int k_len = cur.k_len, n_tiles = cur.n_tiles;
 
-        // ---- Q prologue: lane holds Q[row r16][64 g + c], normalised and rotated, FP32
-        float qf[64];
+        // ---- Q prologue: lane holds Q[row r16][64 g + c(q)] for the wave's QN steps q, with
+        // c(q) = 4 kchunk(q / 4) + q % 4 + 16 half: normalised (the sum of squares over the
+        // whole row) and rotated, FP32. Rotary pair i < 32 / X of the wave is (qv[i], qv[i + NP]),
+        // dims 16 half + i and 32 + 16 half + i (lanes g = 0).
+        constexpr int NP = 32 / X;
+        constexpr int RX = X == 1 ? RUN : 2;   // K chunks per run (two per run in the split layout, for registers)
+        float qv[QN];
         {
-            const f32x4 *qs = (const f32x4 *)(p.qkv + (size_t)t * p.row + (size_t)h * 2 * HD + 64 * g);
+            float ss = 0.f;
+            {
+                const f32x4 *qs = (const f32x4 *)(p.qkv + (size_t)t * p.row + (size_t)h * 2 * HD + 64 * g);
+                float qf[64];
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const f32x4 v = qs[j];
-                qf[4 * j] = v.x; qf[4 * j + 1] = v.y; qf[4 * j + 2] = v.z; qf[4 * j + 3] = v.w;
+                for (int j = 0; j < 16; j++) {
+                    const f32x4 v = qs[j];
+                    qf[4 * j] = v.x; qf[4 * j + 1] = v.y; qf[4 * j + 2] = v.z; qf[4 * j + 3] = v.w;
+                }
+                if (p.q_norm) {
+#pragma unroll
+                    for (int c = 0; c < 64; c++) ss += qf[c] * qf[c];
+                }
+#pragma unroll
+                for (int q = 0; q < QN; q++) {
+                    const int c = 4 * kchunk(q >> 2) + (q & 3);
+                    qv[q] = (X == 1 || half == 0) ? qf[c] : qf[c + 16];
+                }
             }
             if (p.q_norm) {
-                float ss = 0.f;
-#pragma unroll
-                for (int c = 0; c < 64; c++) ss += qf[c] * qf[c];
                 ss += __shfl_xor(ss, 16);
                 ss += __shfl_xor(ss, 32);
                 const float inv = 1.0f / sqrtf(ss / (float)HD + p.eps);
-                const f32x4 *w = (const f32x4 *)(p.q_norm + 64 * g);
+                const float *w = p.q_norm + 64 * g + 16 * half;
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const f32x4 wv = w[j];
+                for (int q4 = 0; q4 < QN / 4; q4++) {
+                    const f32x4 wv = *(const f32x4 *)(w + 4 * kchunk(q4));
 #pragma unroll
-                    for (int e = 0; e < 4; e++) qf[4 * j + e] = qf[4 * j + e] * inv * wv[e];
+                    for (int e = 0; e < 4; e++) qv[4 * q4 + e] = qv[4 * q4 + e] * inv * wv[e];
                 }
             }
             if (p.n_rot && g == 0) {
 #pragma unroll
-                for (int i = 0; i < 32; i++) {
+                for (int i = 0; i < NP; i++) {
+                    const int i0 = NP * half + i;
                     float c, s;
                     if (p.rope_cs) {
-                        const float2 cs = *(const float2 *)(p.rope_cs + ((size_t)t * 32 + i) * 2);
+                        const float2 cs = *(const float2 *)(p.rope_cs + ((size_t)t * 32 + i0) * 2);
                         c = cs.x; s = cs.y;
                     } else {
-                        rope_cs_f32(p.pos3, p.inv_freq, t, i, &c, &s);
+                        rope_cs_f32(p.pos3, p.inv_freq, t, i0, &c, &s);
                     }
-                    const float x0 = qf[i], x1 = qf[i + 32];
-                    qf[i] = x0 * c - x1 * s;
-                    qf[i + 32] = x1 * c + x0 * s;
+                    const float x0 = qv[i], x1 = qv[i + NP];
+                    qv[i] = x0 * c - x1 * s;
+                    qv[i + NP] = x1 * c + x0 * s;
                 }
             }
         }
@@ -285,45 +316,63 @@ __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
         if (n_tiles > 0) clear_tail(cur, 0, smem + 2 * TILE);
         __syncthreads();
 
-        f32x4 o[16];
+        constexpr int NO = 16 / X;   // dim tiles 4j + e of this wave (j < 4 / X)
+        f32x4 o[NO];
 #pragma unroll
-        for (int n = 0; n < 16; n++) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int n = 0; n < NO; n++) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
         float m_run = -INFINITY, l_run = 0.f;
 
         auto tile = [&](const int ti, auto BUF) {
             constexpr int buf = decltype(BUF)::value;
             const int kb = ti * BK;
             if (ti + 1 < n_tiles) fill(cur, kb + BK, smem + (buf ^ 1) * TILE, smem + 2 * TILE + (buf ^ 1) * TILE);
+            // S^T: two 16-key subtiles, QN four-dim steps each, their products interleaved (two
+            // independent accumulator chains); K read in runs of RX chunks per subtile
+            f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
             if (cur.live) {   // wave-uniform: a spare wave of the last head chunk only fills
-                // S^T: two 16-key subtiles, 64 four-dim steps each, their products interleaved
-                // (two independent accumulator chains); K read in runs of RUN chunks per subtile
-                f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-                sfor<NRUN>([&](auto H) {
+                sfor<16 / X / RX>([&](auto H) {
                     constexpr int hh = decltype(H)::value;
-                    f32x4 a[2][RUN];
-                    sfor<RUN>([&](auto J) {
+                    f32x4 a[2][RX];
+                    sfor<RX>([&](auto J) {
                         constexpr int j = decltype(J)::value;
-                        a[0][j] = lds_read_f4<buf * TB + (RUN * hh + j) * 16>(ka);
-                        a[1][j] = lds_read_f4<buf * TB + 16 * ROW * 4 + (RUN * hh + j) * 16>(ka);
+                        constexpr int ch = X == 1 ? RX * hh + j : (RX * hh + j < 4 ? RX * hh + j : RX * hh + j + 4);
+                        a[0][j] = lds_read_f4<buf * TB + ch * 16>(ka);
+                        a[1][j] = lds_read_f4<buf * TB + 16 * ROW * 4 + ch * 16>(ka);
                     });
-                    sfor<RUN>([&](auto J) {
+                    sfor<RX>([&](auto J) {
                         constexpr int j = decltype(J)::value;
-                        lds_wait_f4<2 * (RUN - 1 - j) + 1>(a[0][j]);
-                        lds_wait_f4<2 * (RUN - 1 - j)>(a[1][j]);
+                        lds_wait_f4<2 * (RX - 1 - j) + 1>(a[0][j]);
+                        lds_wait_f4<2 * (RX - 1 - j)>(a[1][j]);
 #pragma unroll
                         for (int e = 0; e < 4; e++) {
-                            s[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0][j][e], qf[4 * (RUN * hh + j) + e], s[0], 0, 0, 0);
-                            s[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1][j][e], qf[4 * (RUN * hh + j) + e], s[1], 0, 0, 0);
+                            s[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0][j][e], qv[4 * (RX * hh + j) + e], s[0], 0, 0, 0);
+                            s[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1][j][e], qv[4 * (RX * hh + j) + e], s[1], 0, 0, 0);
                         }
                     });
                 });
+            }
+            if constexpr (X > 1) {
+                // the halves' partial scores meet: write this wave's, barrier, add the partner's
+                const unsigned xa = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) f32x4 *)(xch + 2 * (wave * 64 + lane));
+                // (the wait states cover an MFMA result read by the LDS write: the compiler does
+                // not see inside the statement)
+                asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4\n\tds_write_b128 %0, %1\n\tds_write_b128 %0, %2 offset:16" : : "v"(xa), "v"(s[0]), "v"(s[1]) : "memory");
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                const unsigned pa = xa + (half ? -1 : 1) * (unsigned)(W * 64 * 32);
+                f32x4 t0, t1;
+                asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)" : "=&v"(t0), "=&v"(t1) : "v"(pa) : "memory");
+                s[0] += t0;
+                s[1] += t1;
+            }
+            if (cur.live) {
                 // V chunk j of step st = (u, v): key 16u + 4v + g, chunk 16j + r16 of its row
                 auto vread = [&](auto ST, auto J) {
                     constexpr int st = decltype(ST)::value, u = st >> 2, v = st & 3, j = decltype(J)::value;
                     return lds_read_f4<buf * TB + (16 * u + 4 * v) * ROW * 4 + 256 * j>(va);
                 };
-                f32x4 vb[4];   // step 0's chunks load while the softmax runs
-                sfor<4>([&](auto J) { vb[decltype(J)::value] = vread(std::integral_constant<int, 0>{}, J); });
+                constexpr int NJ = 4 / X;   // V chunks per step of this wave
+                f32x4 vb[NJ];   // step 0's chunks load while the softmax runs
+                sfor<NJ>([&](auto J) { vb[decltype(J)::value] = vread(std::integral_constant<int, 0>{}, J); });
                 // Online softmax. s[u][v] is the score of key kb + 16u + 4v + g for query row r16.
                 float x[2][4], mx = -INFINITY;
 #pragma unroll
@@ -360,14 +409,14 @@ __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
                 // through four registers: chunk j of the next step is read as soon as the current
                 // step's chunk j has fed its four products, so three reads are always in flight.
 #pragma unroll
-                for (int n = 0; n < 16; n++) o[n] *= alpha_o;
+                for (int n = 0; n < NO; n++) o[n] *= alpha_o;
                 sfor<8>([&](auto S) {
                     constexpr int st = decltype(S)::value, u = st >> 2, v = st & 3;
                     const float b = pv[u][v];
-                    sfor<4>([&](auto J) {
+                    sfor<NJ>([&](auto J) {
                         constexpr int j = decltype(J)::value;
-                        if constexpr (st + 1 < 8) lds_wait_f4<3>(vb[j]);
-                        else lds_wait_f4<3 - j>(vb[j]);
+                        if constexpr (st + 1 < 8) lds_wait_f4<NJ - 1>(vb[j]);
+                        else lds_wait_f4<NJ - 1 - j>(vb[j]);
 #pragma unroll
                         for (int e = 0; e < 4; e++)
                             o[4 * j + e] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb[j][e], b, o[4 * j + e], 0, 0, 0);
@@ -403,8 +452,8 @@ __global__ __launch_bounds__(64 * W) void attn_text_f32_kernel(Params p) {
 #pragma unroll
             for (int v = 0; v < 4; v++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int d = 64 * j + 16 * g + 4 * v;
+                for (int j = 0; j < 4 / X; j++) {
+                    const int d = 64 * (j + (4 / X) * half) + 16 * g + 4 * v;
                     f32x4 w;
 #pragma unroll
                     for (int e = 0; e < 4; e++) w[e] = o[4 * j + e][v] * il;
