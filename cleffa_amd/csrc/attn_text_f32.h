@@ -14,9 +14,10 @@
 // accumulation), the softmax in FP32 VALU. Key tiles start at the record's first key, so a
 // record's arithmetic does not depend on what is packed with it.
 //
-// Workgroup: one wave per q head of a chunk of the GQA group (W <= 8 waves; a group of more
-// than 8 heads runs as several chunks), all on the same 16 query rows, so one 32-key K / V tile
-// in LDS (64 KB, double buffered: 128 KB) serves the chunk.
+// Workgroup: a chunk of W <= 8 q heads of the GQA group (a group of more than 8 heads runs as
+// several chunks), X = 1 or 2 waves per head, all on the same 16 query rows, so one 32-key K / V
+// tile in LDS (64 KB, double buffered: 128 KB) serves the chunk. With two waves per head each
+// takes half of the head dims (see attn_text_f32_kernel).
 //   S^T = K . Q^T      A = 16 keys x 4 dims of K (LDS), B = the wave's Q (registers).
 //   O^T += V^T . P^T   A = 16 dims x 4 keys of V (LDS), B = P (registers).
 // Lane l = 16 g + r. S^T's A row r takes key 4(r % 4) + r / 4 of the 16-key subtile, so the four
