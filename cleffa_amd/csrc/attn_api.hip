@@ -520,10 +520,11 @@ bool clef_hip_attn_prep_kv(const clef_hip_attn_args *a, void *stream, char *err,
         return launch_ok("text_prep_kv_f32", err, errlen);
     }
     if (!a->tok_kv) return fail(err, errlen, "the K/V prologue needs tok_kv (the plan's pass row -> plane row map)");
-    dim3 grid((a->T + kPrepRowsBM - 1) / kPrepRowsBM, 2 * a->nkv);
-    hipLaunchKernelGGL(text_prep_rows_kernel, grid, dim3(kPrepRowsThreads), 0, (hipStream_t)stream, (const uint16_t *)a->qkv,
-                       a->row, kv_rows_params(a, a->tok_kv));
-    return launch_ok("text_prep_rows", err, errlen);
+    // K waves of 4 pass rows, then V waves of (kv head, 64 rows, 16 dims); 4 waves per workgroup
+    const long waves = (long)(a->T + 3) / 4 + (long)a->nkv * ((a->T + 63) / 64) * 16;
+    hipLaunchKernelGGL(text_prep_direct_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(kPrepDirectThreads), 0, (hipStream_t)stream,
+                       (const uint16_t *)a->qkv, a->row, kv_rows_params(a, a->tok_kv));
+    return launch_ok("text_prep_direct", err, errlen);
 }
 
 bool clef_hip_attn_core(const clef_hip_attn_args *a, void *stream, char *err, size_t errlen) {

@@ -18,7 +18,7 @@
 //             accumulators are four consecutive columns of one output row.
 //   epilogue: accumulators rounded to bf16 into an LDS copy of the tile, then coalesced row
 //             stores; K and V tiles take the prologue from that copy, so their planes hold
-//             bitwise what text_prep_rows_kernel makes of the same bf16 rows (both run kv_rows.h).
+//             bitwise what text_prep_direct_kernel makes of the same bf16 rows (both run kv_rows.h).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>

@@ -4,9 +4,9 @@
 // K and V) and 857-928 (split16 and attn_prep_split: the f16 planes, |x| > f16_lim or NaN
 // saturating and flagging the record).
 //
-// Two producers fill the tile: text_prep_rows_kernel (attn_kernels.h) loads it from the qkv
-// rows, and the QKV GEMM (gemm_kernel.h) leaves its bf16 output tile there; both then call these
-// functions, so the planes they write are bitwise the same.
+// Two producers: the QKV GEMM (gemm_kernel.h) leaves its bf16 output tile in LDS and runs k_rows /
+// v_rows on it; text_prep_direct_kernel reads the qkv rows straight into registers. Both go through
+// k_row_out, rope_sincos and v_word, so the planes they write are bitwise the same.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -56,6 +56,86 @@ __device__ __forceinline__ void k_table(const KvRows &p, int m0, int row, int k,
 __device__ __forceinline__ int k_lane_dim(int k, int h) {   // first dim of the lane's half h (8 dims)
     return k < 4 ? 8 * k + 32 * h : 64 + 16 * (k - 4) + 8 * h;
 }
+// One K row's arithmetic, lane k of its 16 (dims d(k, 0..15) as above, the row's bf16 values in
+// kw0 / kw1): RMSNorm with the lane's weights wn, the rotary turn of the lane's pairs with their
+// (cos, sin) in c4 (lanes k < 4; c4[q] holds pairs 8k + 2q and 8k + 2q + 1), split16's
+// saturation and flag, and the f16 stores to plane row tok_kv[t]. All 16 lanes of the row call it
+// together (the sum of squares is a row-wide DPP sum). Every producer of the K plane goes through
+// here, so the planes come out bitwise the same whichever wrote them.
+__device__ __forceinline__ void k_row_out(const KvRows &p, const u32x4 &kw0, const u32x4 &kw1, const float (&wn)[16],
+                                          const float4 (&c4)[4], int k, int t, int kh) {
+    constexpr int HD = 256;
+    const int d0 = k_lane_dim(k, 0), d1 = k_lane_dim(k, 1);
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        x[2 * j] = bf_lo(kw0[j]);
+        x[2 * j + 1] = bf_hi(kw0[j]);
+        x[8 + 2 * j] = bf_lo(kw1[j]);
+        x[8 + 2 * j + 1] = bf_hi(kw1[j]);
+    }
+    if (p.k_norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) ss += x[e] * x[e];
+        ss = row16_sum(ss);
+        const float inv = rsqrtf(ss / (float)HD + p.eps);
+#pragma unroll
+        for (int e = 0; e < 16; e++) x[e] *= inv * wn[e];
+    }
+    if (p.n_rot && k < 4) {   // pair 8k + e: x[e] turns with x[e + 8]
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int e = 2 * q + h;
+                const float cn = h ? c4[q].z : c4[q].x, sn = h ? c4[q].w : c4[q].y;
+                const float x0 = x[e], x1 = x[e + 8];
+                x[e] = x0 * cn - x1 * sn;
+                x[e + 8] = x1 * cn + x0 * sn;
+            }
+        }
+    }
+    // split16's saturation: the largest magnitude decides (NaN propagates through the maximum,
+    // and fails the compare); only a row holding one takes the elementwise pass
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; e += 2)
+        amax = __builtin_elementwise_maximum(amax, __builtin_elementwise_maximum(fabsf(x[e]), fabsf(x[e + 1])));
+    if (!(amax <= p.f16_lim)) {
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            if (!(fabsf(x[e]) <= p.f16_lim)) x[e] = copysignf(65504.f, x[e]);
+        if (p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    uint16_t *dst = p.k_plane + ((size_t)kh * p.kvT + p.tok_kv[t]) * HD;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const float *xs = x + 8 * h;
+        u32x4 ko = {pack_f16(xs[0], xs[1]), pack_f16(xs[2], xs[3]), pack_f16(xs[4], xs[5]), pack_f16(xs[6], xs[7])};
+        *(u32x4 *)(dst + (h ? d1 : d0)) = ko;
+    }
+}
+
+// the lane's k_norm weights, in its dim order
+__device__ __forceinline__ void k_lane_weights(const KvRows &p, int k, float (&wn)[16]) {
+    const int d0 = k_lane_dim(k, 0), d1 = k_lane_dim(k, 1);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float4 w4 = *(const float4 *)(p.k_norm + ((q < 2) ? d0 : d1) + 4 * (q & 1));
+        wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
+    }
+}
+
+// A V word (two bf16 of one row) through split16's check: |v| > f16_lim or NaN saturates to
+// +-65536 (bf16's rounding of 65504); returns whether any did.
+__device__ __forceinline__ bool v_word(unsigned &w, float lim) {
+    const bool lo_bad = !(__uint_as_float((w & 0x7fffu) << 16) <= lim), hi_bad = !(__uint_as_float(w & 0x7fff0000u) <= lim);
+    if (lo_bad) w = (w & 0xffff8000u) | 0x4780u;
+    if (hi_bad) w = (w & 0x8000ffffu) | 0x47800000u;
+    return lo_bad | hi_bad;
+}
+
 template <int NTHREADS, int BM, bool TABLED = false>
 __device__ __forceinline__ void k_rows(const KvRows &p, const uint8_t *ct, int cs, int m0, int kh, float2 *table) {
     static_assert(!TABLED || NTHREADS / 16 == BM, "a caller-filled table covers one pass");
@@ -64,13 +144,7 @@ __device__ __forceinline__ void k_rows(const KvRows &p, const uint8_t *ct, int c
     const int half_rot = p.n_rot / 2;   // 0 or 32: dims [0, 32) pair with [32, 64)
     const int d0 = k_lane_dim(k, 0), d1 = k_lane_dim(k, 1);
     float wn[16];
-    if (p.k_norm) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 w4 = *(const float4 *)(p.k_norm + ((q < 2) ? d0 : d1) + 4 * (q & 1));
-            wn[4 * q] = w4.x; wn[4 * q + 1] = w4.y; wn[4 * q + 2] = w4.z; wn[4 * q + 3] = w4.w;
-        }
-    }
+    if (p.k_norm) k_lane_weights(p, k, wn);
     for (int pass = 0; pass < BM / RPP; pass++) {
         const int row = RPP * pass + rr, t = m0 + row;
         const bool valid = t < p.T;
@@ -80,57 +154,13 @@ __device__ __forceinline__ void k_rows(const KvRows &p, const uint8_t *ct, int c
         }
         if (valid) {
             const u32x4 kw0 = *(const u32x4 *)(ct + row * cs + 2 * d0), kw1 = *(const u32x4 *)(ct + row * cs + 2 * d1);
-            float x[16];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                x[2 * j] = bf_lo(kw0[j]);
-                x[2 * j + 1] = bf_hi(kw0[j]);
-                x[8 + 2 * j] = bf_lo(kw1[j]);
-                x[8 + 2 * j + 1] = bf_hi(kw1[j]);
-            }
-            if (p.k_norm) {
-                float ss = 0.f;
-#pragma unroll
-                for (int e = 0; e < 16; e++) ss += x[e] * x[e];
-                ss = row16_sum(ss);
-                const float inv = rsqrtf(ss / (float)HD + p.eps);
-#pragma unroll
-                for (int e = 0; e < 16; e++) x[e] *= inv * wn[e];
-            }
-            if (half_rot && k < 4) {   // pair 8k + e: x[e] turns with x[e + 8]
+            float4 c4[4] = {};
+            if (half_rot && k < 4) {
                 const float4 *c = (const float4 *)(table + 32 * rr + 8 * k);
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float4 cs2 = c[q];   // (cos, sin) of pairs 8k + 2q, 8k + 2q + 1
-#pragma unroll
-                    for (int h = 0; h < 2; h++) {
-                        const int e = 2 * q + h;
-                        const float cn = h ? cs2.z : cs2.x, sn = h ? cs2.w : cs2.y;
-                        const float x0 = x[e], x1 = x[e + 8];
-                        x[e] = x0 * cn - x1 * sn;
-                        x[e + 8] = x1 * cn + x0 * sn;
-                    }
-                }
+                for (int q = 0; q < 4; q++) c4[q] = c[q];
             }
-            // split16's saturation: the largest magnitude decides (NaN propagates through the
-            // maximum, and fails the compare); only a row holding one takes the elementwise pass
-            float amax = 0.f;
-#pragma unroll
-            for (int e = 0; e < 16; e += 2)
-                amax = __builtin_elementwise_maximum(amax, __builtin_elementwise_maximum(fabsf(x[e]), fabsf(x[e + 1])));
-            if (!(amax <= p.f16_lim)) {
-#pragma unroll
-                for (int e = 0; e < 16; e++)
-                    if (!(fabsf(x[e]) <= p.f16_lim)) x[e] = copysignf(65504.f, x[e]);
-                if (p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            uint16_t *dst = p.k_plane + ((size_t)kh * p.kvT + p.tok_kv[t]) * HD;
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const float *xs = x + 8 * h;
-                u32x4 ko = {pack_f16(xs[0], xs[1]), pack_f16(xs[2], xs[3]), pack_f16(xs[4], xs[5]), pack_f16(xs[6], xs[7])};
-                *(u32x4 *)(dst + (h ? d1 : d0)) = ko;
-            }
+            k_row_out(p, kw0, kw1, wn, c4, k, t, kh);
         }
         if (half_rot && !TABLED) __syncthreads();   // the table is read before the next pass rewrites it
     }
@@ -155,11 +185,7 @@ __device__ __forceinline__ void v_rows(const KvRows &p, const uint8_t *ct, int c
 #pragma unroll 8
         for (int d = 0; d < DPT; d += 2) {
             unsigned w = *(const unsigned *)(ct + row * cs + 2 * (d0 + d));
-            const bool lo_bad = !(__uint_as_float((w & 0x7fffu) << 16) <= p.f16_lim),
-                       hi_bad = !(__uint_as_float(w & 0x7fff0000u) <= p.f16_lim);
-            if (lo_bad) w = (w & 0xffff8000u) | 0x4780u;
-            if (hi_bad) w = (w & 0x8000ffffu) | 0x47800000u;
-            bad |= lo_bad | hi_bad;
+            bad |= v_word(w, p.f16_lim);
             col[(size_t)d * p.kvT] = (uint16_t)w;
             col[(size_t)(d + 1) * p.kvT] = (uint16_t)(w >> 16);
         }
@@ -167,36 +193,91 @@ __device__ __forceinline__ void v_rows(const KvRows &p, const uint8_t *ct, int c
     }
 }
 
-// The K/V prologue as its own kernel, over pass rows: workgroup (b, j) loads rows 64b .. 64b + 63
-// of K head j (j < nkv) or V head j - nkv into LDS and runs k_rows / v_rows on them. All loads
-// are issued at once (no load depends on another), a K workgroup fills its rotary table while
-// they land, and the plane rows come from tok_kv.
-constexpr int kPrepRowsBM = 64, kPrepRowsThreads = 1024, kPrepRowsCS = 512 + 16;
-__global__ __launch_bounds__(kPrepRowsThreads) void text_prep_rows_kernel(const uint16_t *qkv, int row_len, KvRows p) {
-    constexpr int BM = kPrepRowsBM, NT = kPrepRowsThreads, CSB = kPrepRowsCS;
-    __shared__ __attribute__((aligned(16))) uint8_t tile[BM * CSB];
-    __shared__ __attribute__((aligned(16))) float2 table[NT / 16 * 32];
-    const int tid = threadIdx.x, m0 = blockIdx.x * BM, j = blockIdx.y;
-    const bool is_k = j < p.nkv;
-    const int head = is_k ? j : j - p.nkv;
-    const uint16_t *src = qkv + (size_t)p.nh * 2 * 256 + (size_t)(is_k ? 0 : p.nkv * 256) + (size_t)head * 256;
-    constexpr int PER = BM * 32 / NT;
-    u32x4 w[PER];
+// The K/V prologue as its own kernel with no LDS tile and no barrier: every wave works alone,
+// so the loads of some waves overlap the stores of others, as in a copy kernel.
+//  - K waves (the first n_kwaves): 4 pass rows, 16 lanes each, every kv head. A lane's loads for
+//    all its kv heads go out first; meanwhile it computes the rotary cos/sin of pairs 2k and
+//    2k + 1 of its row (k_table's arithmetic; rope_cs gets them once per row), and the lanes
+//    k < 4 fetch the four pairs-of-pairs they turn from lanes 4k .. 4k + 3 with ds_bpermute.
+//    Then k_row_out per kv head.
+//  - V waves: 64 pass rows (lane = row) x 16 dims of one kv head: two 16-byte loads, then 16
+//    two-byte stores, each one 128-byte V^T line, through split16's check.
+// Planes, flags and rope_cs are bitwise those of the QKV GEMM's epilogue (the same k_row_out,
+// rope_sincos and v_word).
+constexpr int kPrepDirectThreads = 256, kPrepDirectKvChunk = 4;
+__device__ __forceinline__ int prep_direct_kwaves(int T) { return (T + 3) / 4; }
+__device__ __forceinline__ float bperm(int src_lane, float v) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(4 * src_lane, __float_as_int(v)));
+}
+__global__ __launch_bounds__(kPrepDirectThreads) void text_prep_direct_kernel(const uint16_t *qkv, int row_len, KvRows p) {
+    constexpr int HD = 256, KC = kPrepDirectKvChunk;
+    const int lane = threadIdx.x & 63;
+    const int gw = (int)blockIdx.x * (kPrepDirectThreads / 64) + (int)(threadIdx.x >> 6);
+    const int n_kwaves = prep_direct_kwaves(p.T);
+    if (gw < n_kwaves) {
+        const int rr = lane >> 4, k = lane & 15, t = gw * 4 + rr;
+        const bool valid = t < p.T;
+        const int tt = valid ? t : p.T - 1;   // rows past the pass load the last row, then stop
+        const int d0 = k_lane_dim(k, 0), d1 = k_lane_dim(k, 1);
+        const uint16_t *src = qkv + (size_t)tt * row_len + (size_t)p.nh * 2 * HD;
+        u32x4 kw[KC][2];
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-        const int id = tid + NT * i, r = id >> 5, c16 = id & 31;
-        const int t = min(m0 + r, p.T - 1);
-        w[i] = *(const u32x4 *)(src + (size_t)t * row_len + 8 * c16);
-    }
-    if (is_k && p.n_rot) k_table(p, m0, tid >> 4, tid & 15, head, table);
+        for (int j = 0; j < KC; j++) {
+            const int kh = min(j, p.nkv - 1);
+            kw[j][0] = *(const u32x4 *)(src + (size_t)kh * HD + d0);
+            kw[j][1] = *(const u32x4 *)(src + (size_t)kh * HD + d1);
+        }
+        float wn[16];
+        if (p.k_norm) k_lane_weights(p, k, wn);
+        float4 c4[4] = {};
+        if (p.n_rot) {
+            float cs[4];
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-        const int id = tid + NT * i, r = id >> 5, c16 = id & 31;
-        *(u32x4 *)(tile + r * CSB + 16 * c16) = w[i];
+            for (int h = 0; h < 2; h++) {
+                const int i = 2 * k + h;
+                const float ang = (float)p.pos3[3 * (size_t)tt + i % 3] * p.inv_freq[i];
+                rope_sincos(ang, &cs[2 * h + 1], &cs[2 * h]);
+            }
+            if (valid && p.rope_cs) *(float4 *)(p.rope_cs + (size_t)t * 64 + 4 * k) = make_float4(cs[0], cs[1], cs[2], cs[3]);
+            const int base = 16 * rr + 4 * (k & 3);
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                c4[q] = make_float4(bperm(base + q, cs[0]), bperm(base + q, cs[1]), bperm(base + q, cs[2]), bperm(base + q, cs[3]));
+        }
+        if (!valid) return;
+        for (int kh0 = 0; kh0 < p.nkv; kh0 += KC) {
+            if (kh0 > 0) {
+#pragma unroll
+                for (int j = 0; j < KC; j++) {
+                    const int kh = min(kh0 + j, p.nkv - 1);
+                    kw[j][0] = *(const u32x4 *)(src + (size_t)kh * HD + d0);
+                    kw[j][1] = *(const u32x4 *)(src + (size_t)kh * HD + d1);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < KC; j++)
+                if (kh0 + j < p.nkv) k_row_out(p, kw[j][0], kw[j][1], wn, c4, k, t, kh0 + j);
+        }
+        return;
     }
-    __syncthreads();
-    if (is_k) k_rows<NT, BM, true>(p, tile, CSB, m0, head, table);
-    else v_rows<NT / 64, BM>(p, tile, CSB, m0, head);
+    // V: task (kv head, 64-row block, 16-dim group)
+    const int gv = gw - n_kwaves, n_rb = (p.T + 63) / 64;
+    if (gv >= p.nkv * n_rb * 16) return;
+    const int dg = gv & 15, rb = (gv >> 4) % n_rb, kh = (gv >> 4) / n_rb;
+    const int t = rb * 64 + lane;
+    if (t >= p.T) return;
+    const uint16_t *src = qkv + (size_t)t * row_len + (size_t)p.nh * 2 * HD + (size_t)p.nkv * HD + (size_t)kh * HD + 16 * dg;
+    const u32x4 v0 = *(const u32x4 *)src, v1 = *(const u32x4 *)(src + 8);
+    uint16_t *col = p.vt_plane + ((size_t)kh * HD + 16 * dg) * p.kvT + (size_t)p.tok_kv[t];
+    bool bad = false;
+#pragma unroll
+    for (int d = 0; d < 16; d += 2) {
+        unsigned w = d < 8 ? v0[d / 2] : v1[(d - 8) / 2];
+        bad |= v_word(w, p.f16_lim);
+        col[(size_t)d * p.kvT] = (uint16_t)w;
+        col[(size_t)(d + 1) * p.kvT] = (uint16_t)(w >> 16);
+    }
+    if (bad && p.ovf && p.seq_start) __hip_atomic_store(p.ovf + p.seq_start[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace clef_hip
