@@ -111,6 +111,17 @@ def test_edge_lengths_packed():
     assert_close(out.float().cpu().numpy(), oracle_text(w), what="edge lengths")
 
 
+@pytest.mark.parametrize("nh,nkv", [(16, 8), (10, 5)])
+def test_more_than_four_kv_heads(nh, nkv):
+    """More kv heads than the K/V prologue's K waves load at once (4): its second round of loads
+    (8 kv heads), and a last round with one kv head (5), against float64."""
+    _say(f"[parity] {nh}/{nkv} heads")
+    w = workloads.text_inputs([1, 63, 130, 300], nh, nkv, seed=nh)
+    w.update(gate=True, theta=1e7)
+    out, _ = gpu_text(w)
+    assert_close(out.float().cpu().numpy(), oracle_text(w), what=f"{nh}/{nkv}")
+
+
 def test_packing_invariance_bitwise():
     """Each record's output equals the same record run alone, bit for bit
     (bench/attention_bench.m:263-308)."""
