@@ -156,13 +156,19 @@ struct ItemList {
         // fingerprint the plan wrote into word 7 of every block entry. Otherwise every
         // workgroup (all read the same words) takes the static order, which covers every item.
         if (p.sched) {
+            // the header and the plan's fingerprint in one round trip, then the workgroup's two
+            // offsets in one
             i32x8 h;
-            asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(h) : "s"(p.sched) : "memory");
-            const int fp = sload(p.blocks + 7);
+            int fp;
+            asm volatile("s_load_dwordx8 %0, %2, 0x0\n\ts_load_dword %1, %3, 0x1c\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&s"(h), "=&s"(fp) : "s"(p.sched), "s"(p.blocks) : "memory");
             if (h[0] == 0x53434844 && h[1] == p.n_blk && h[2] == p.nh && h[3] == (int)gridDim.x && h[4] == p.nkv && h[5] == fp) {
                 const int32_t *offs = p.sched + 8;
-                s0 = sload(offs + blockIdx.x);
-                s1 = sload(offs + blockIdx.x + 1);
+                typedef __attribute__((ext_vector_type(2))) int i32x2;
+                i32x2 o;
+                asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(o) : "s"(offs + blockIdx.x) : "memory");
+                s0 = o[0];
+                s1 = o[1];
                 list = offs + gridDim.x + 1;
             }
         }
