@@ -298,7 +298,7 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
     const int groups = (xh && n_wg % 8 == 0) ? 8 : 1;
     auto cost_of = [&](int item) {
         const int32_t *e = blocks + 8 * ((item & ((1 << 28) - 1)) / nh);
-        const int k_len = (item >> 28) == 1 ? std::min(e[4], e[2] + 64) : e[4];
+        const int k_len = ((item >> 28) & 3) == 1 ? std::min(e[4], e[2] + 64) : e[4];
         return (k_len + 63) / 64 + kFixed;
     };
     // Every item with its cost; then each to an XCD group: its head's, or for a packed item whose
@@ -310,11 +310,19 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
         // a block of at most 64 rows runs k heads of a kv group at once (unless the pass splits
         // blocks, which wants more items, not fewer)
         const int pk = split ? 1 : clef_hip::pack_heads(blocks[8 * bi + 1], nh / nkv);
+        // a block of more than 64 rows runs as its two halves for two heads each (bit 30) when
+        // the kv group has an even size
+        const bool pair = !split && blocks[8 * bi + 1] > 64 && (nh / nkv) % 2 == 0;
         for (int h = 0; h < nh; h++) {
             const int it = bi * nh + h;
             if (split && blocks[8 * bi + 1] > 64) {   // the block's rows 0-63 and 64-127
                 all.push_back({cost_of(it | (1 << 28)), it | (1 << 28)});
                 all.push_back({cost_of(it | (2 << 28)), it | (2 << 28)});
+            } else if (pair) {                        // heads h, h + 1: rows 0-63, then 64-127
+                if (h % 2 == 0) {
+                    all.push_back({cost_of(it | (1 << 28) | (1 << 30)), it | (1 << 28) | (1 << 30)});
+                    all.push_back({cost_of(it | (2 << 28) | (1 << 30)), it | (2 << 28) | (1 << 30)});
+                }
             } else if (pk > 1) {                      // heads h .. h + pk - 1 (group-aligned)
                 if (h % pk == 0) all.push_back({cost_of(it | (3 << 28)), it | (3 << 28)});
             } else {
@@ -329,7 +337,8 @@ bool clef_hip_attn_schedule(const int32_t *blocks, int n_blk, int nh, int nkv, i
         int x = 0;
         if (groups != 1) {
             const int base = c.second & ((1 << 28) - 1), h0 = base % nh;
-            const int hk = (c.second >> 28) == 3 ? clef_hip::pack_heads(blocks[8 * (base / nh) + 1], nh / nkv) : 1;
+            const int hk = ((c.second >> 28) & 3) == 3 ? clef_hip::pack_heads(blocks[8 * (base / nh) + 1], nh / nkv)
+                                                      : ((c.second >> 30) & 1) ? 2 : 1;
             x = h0 / xh;
             for (int y = h0 / xh + 1; y <= (h0 + hk - 1) / xh; y++)
                 if (xload[y] < xload[x]) x = y;

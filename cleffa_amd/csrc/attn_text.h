@@ -127,8 +127,10 @@ __device__ __forceinline__ int sload(const int32_t *ptr) {
 // covers: 0 all, 1 rows 0-63, 2 rows 64-127 (a pass with fewer items than workgroups splits its
 // blocks so that every workgroup has work), or 3: the block's rows (at most 64) for heads
 // h .. h + k - 1 of one kv group, ceil(rows / 16) waves per head (pack_heads), which share its
-// key tiles. A row's arithmetic does not depend on any of this: each 16-row wave runs the key
-// tiles up to its own last row, from the record's first key.
+// key tiles. Bit 30 with code 1 or 2: that half of the block for heads h and h + 1 of one kv
+// group (four waves per head), so that a causal block's last 64 keys, which only its rows 64-127
+// see, run on a full workgroup. A row's arithmetic does not depend on any of this: each 16-row
+// wave runs the key tiles up to its own last row, from the record's first key.
 constexpr int kItemBits = 28;
 __device__ __forceinline__ int item_base(int it) { return it & ((1 << kItemBits) - 1); }
 // Heads per packed item of a block of nq <= 64 rows: the largest divisor of the kv group size
@@ -253,7 +255,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     // once the kernel has stored anything, and those would wait behind the in-flight tile fills.
     auto decode_from = [&](const i32x8 &e, int it) {
         Item s;
-        const int base = item_base(it), half = it >> kItemBits;
+        const int base = item_base(it), half = (it >> kItemBits) & 3, pair = (it >> 30) & 1;
         const int bi = base / p.nh;
         s.h = base - bi * p.nh;
         s.q_row0 = e[0]; s.nq = e[1]; s.q_pos0 = e[2]; s.k_row0 = e[3]; s.k_len = e[4];
@@ -265,8 +267,8 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         }
         const int group = p.nh / p.nkv;
         s.wph = 8; s.hk = 1;
-        if (half == 3) {   // heads h .. h + k - 1, all in h's kv group (else the item runs head h)
-            const int k = pack_heads(s.nq, group);
+        if (half == 3 || pair) {   // heads h .. h + k - 1, all in h's kv group (else the item runs head h)
+            const int k = pair ? ((group % 2 == 0 && s.nq <= 64) ? 2 : 1) : pack_heads(s.nq, group);
             if (k > 1 && s.h % group + k <= group) { s.wph = (s.nq + 15) / 16; s.hk = k; }
         }
         s.flag_row = e[5];
@@ -363,7 +365,7 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
     for (int k = 0;; k++) {
         // trace row of this item (100 MHz wall clock): start, end, HW_ID, XCC_ID, prologue end,
         // key loop end, workgroup, ordinal within the workgroup
-        uint64_t *const tr = (p.trace && tid == 0 && (item >> kItemBits) != 2) ? p.trace + 8 * (size_t)item_base(item) : nullptr;
+        uint64_t *const tr = (p.trace && tid == 0 && ((item >> kItemBits) & 3) != 2) ? p.trace + 8 * (size_t)item_base(item) : nullptr;
         if (tr) {
             tr[0] = wall_clock64();
             tr[2] = __builtin_amdgcn_s_getreg((31 << 11) | 4);
