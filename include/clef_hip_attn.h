@@ -170,7 +170,9 @@ typedef struct {
  * rows becomes two items, 1 (rows 0-63) and 2 (rows 64-127), so that more workgroups have work;
  * otherwise a block of at most 64 rows runs k heads h .. h + k - 1 of one kv group in one item,
  * 3 (k the largest divisor of nh / nkv with k * ceil(rows / 16) <= 8), so that they share its key
- * tiles. Outputs are bitwise the same in every case (a code 2 of a block of 64 rows or fewer runs
+ * tiles, and when nh / nkv is even a block of more than 64 rows runs as two items for heads h and
+ * h + 1, codes 1 and 2 with bit 30 set (a causal block's last 64 keys, which only its rows 64-127
+ * see, then run on a full workgroup). Outputs are bitwise the same in every case (a code 2 of a block of 64 rows or fewer runs
  * the whole block, a code 3 that does not fit its kv group runs head h only, so no list reaches
  * rows or heads outside its item). clef_hip_attn_sched_size gives the room to allocate (an upper
  * bound: the last offset is the item count). */
