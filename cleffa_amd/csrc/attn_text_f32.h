@@ -11,7 +11,7 @@
 //   that saturates and flags the record) or as f32.
 //
 // Everything is FP32: the products run on v_mfma_f32_16x16x4f32 (FP32 operands, FP32
-// accumulation), the softmax in FP32 VALU. Key tiles start at the record's first key, so a
+// accumulation), the softmax in FP32 VALU (exp2 domain). Key tiles start at the record's first key, so a
 // record's arithmetic does not depend on what is packed with it.
 //
 // Workgroup: a chunk of W <= 8 q heads of the GQA group (a group of more than 8 heads runs as
@@ -312,6 +312,10 @@ __global__ __launch_bounds__(64 * W * X) void attn_text_f32_kernel(Params p) {
                     qv[i + NP] = x1 * c + x0 * s;
                 }
             }
+            // the scores in the exp2 domain: scale * log2 e folded into Q
+            const float sl2 = p.scale * 1.4426950408889634f;
+#pragma unroll
+            for (int q = 0; q < QN; q++) qv[q] *= sl2;
         }
         __builtin_amdgcn_s_waitcnt(0);
         if (n_tiles > 0) clear_tail(cur, 0, smem + 2 * TILE);
@@ -382,19 +386,19 @@ __global__ __launch_bounds__(64 * W * X) void attn_text_f32_kernel(Params p) {
                     for (int v = 0; v < 4; v++) {
                         const int key = kb + 16 * u + 4 * v + g;
                         const bool ok = q_valid && key < k_len && (!p.causal || key <= qpos);
-                        x[u][v] = ok ? s[u][v] * p.scale : -INFINITY;
+                        x[u][v] = ok ? s[u][v] : -INFINITY;
                         mx = fmaxf(mx, x[u][v]);
                     }
                 const float mn = fmaxf(m_run, xrow_max(mx));
                 float pv[2][4];
                 float alpha = 1.f, rs = 0.f;
                 if (mn != -INFINITY) {
-                    alpha = (m_run == -INFINITY) ? 0.f : expf(m_run - mn);
+                    alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - mn);
 #pragma unroll
                     for (int u = 0; u < 2; u++)
 #pragma unroll
                         for (int v = 0; v < 4; v++) {
-                            pv[u][v] = x[u][v] == -INFINITY ? 0.f : expf(x[u][v] - mn);
+                            pv[u][v] = x[u][v] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x[u][v] - mn);
                             rs += pv[u][v];
                         }
                 } else {
