@@ -267,26 +267,32 @@ __global__ __launch_bounds__(64 * W * X) void attn_text_f32_kernel(Params p) {
         {
             float ss = 0.f;
             {
-                const f32x4 *qs = (const f32x4 *)(p.qkv + (size_t)t * p.row + (size_t)h * 2 * HD + 64 * g);
-                float qf[64];
+                // the wave's own QN elements of the lane's 64 (the chunks kchunk(q4) + 4 half)
+                const float *qs = p.qkv + (size_t)t * p.row + (size_t)h * 2 * HD + 64 * g + 16 * half;
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const f32x4 v = qs[j];
-                    qf[4 * j] = v.x; qf[4 * j + 1] = v.y; qf[4 * j + 2] = v.z; qf[4 * j + 3] = v.w;
+                for (int q4 = 0; q4 < QN / 4; q4++) {
+                    const f32x4 v = *(const f32x4 *)(qs + 4 * kchunk(q4));
+                    qv[4 * q4] = v.x; qv[4 * q4 + 1] = v.y; qv[4 * q4 + 2] = v.z; qv[4 * q4 + 3] = v.w;
                 }
                 if (p.q_norm) {
 #pragma unroll
-                    for (int c = 0; c < 64; c++) ss += qf[c] * qf[c];
-                }
-#pragma unroll
-                for (int q = 0; q < QN; q++) {
-                    const int c = 4 * kchunk(q >> 2) + (q & 3);
-                    qv[q] = (X == 1 || half == 0) ? qf[c] : qf[c + 16];
+                    for (int q = 0; q < QN; q++) ss += qv[q] * qv[q];
                 }
             }
             if (p.q_norm) {
                 ss += __shfl_xor(ss, 16);
                 ss += __shfl_xor(ss, 32);
+                if constexpr (X > 1) {
+                    // the two halves' sums of squares meet through LDS: the row's sum is the same
+                    // in both (own + partner's)
+                    float *xs = (float *)xch;
+                    asm volatile("ds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier"
+                                 : : "v"((unsigned)(uintptr_t)(const __attribute__((address_space(3))) float *)(xs + wave * 64 + lane)), "v"(ss) : "memory");
+                    float o;
+                    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                                 : "=v"(o) : "v"((unsigned)(uintptr_t)(const __attribute__((address_space(3))) float *)(xs + (half ? wave - W : wave + W) * 64 + lane)) : "memory");
+                    ss = half ? o + ss : ss + o;
+                }
                 const float inv = 1.0f / sqrtf(ss / (float)HD + p.eps);
                 const float *w = p.q_norm + 64 * g + 16 * half;
 #pragma unroll
@@ -465,7 +471,7 @@ __global__ __launch_bounds__(64 * W * X) void attn_text_f32_kernel(Params p) {
                     if (p.gate) {
                         const f32x4 gv = *(const f32x4 *)(grow + d);
 #pragma unroll
-                        for (int e = 0; e < 4; e++) w[e] = w[e] * (1.0f / (1.0f + expf(-gv[e])));
+                        for (int e = 0; e < 4; e++) w[e] = w[e] * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gv[e] * 1.4426950408889634f));
                     }
                     store_out4(p.out, obase + d, w, p.out_type, p.f16_lim, done.flag);
                 }
