@@ -284,9 +284,9 @@ __global__ __launch_bounds__(64 * W * X) void attn_text_f32_kernel(Params p) {
                 ss += __shfl_xor(ss, 32);
                 if constexpr (X > 1) {
                     // the two halves' sums of squares meet through LDS: the row's sum is the same
-                    // in both (own + partner's)
+                    // in both (own + partner's); the nop covers a VALU result read by the LDS write
                     float *xs = (float *)xch;
-                    asm volatile("ds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier"
+                    asm volatile("s_nop 1\n\tds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier"
                                  : : "v"((unsigned)(uintptr_t)(const __attribute__((address_space(3))) float *)(xs + wave * 64 + lane)), "v"(ss) : "memory");
                     float o;
                     asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)"
