@@ -122,6 +122,19 @@ def test_more_than_four_kv_heads(nh, nkv):
     assert_close(out.float().cpu().numpy(), oracle_text(w), what=f"{nh}/{nkv}")
 
 
+def test_text_bidirectional_packed():
+    """A bidirectional text pass (plan causal=False) through the tensor core: each record's rows
+    see all its keys, including the blocks of more than 64 rows that run as paired halves;
+    against float64, and one-workgroup-per-item order bitwise equal to the scheduled grid."""
+    _say("[parity] text bidirectional")
+    w = workloads.text_inputs([200, 1, 65, 130], 12, 2, seed=21)
+    w.update(gate=True, theta=1e7)
+    out, _ = gpu_text(w, causal=False)
+    assert_close(out.float().cpu().numpy(), oracle_text(w, causal=False), what="bidirectional")
+    alone, _ = gpu_text(w, causal=False, schedule=False)
+    assert torch.equal(out.cpu().view(torch.int16), alone.cpu().view(torch.int16))
+
+
 def test_packing_invariance_bitwise():
     """Each record's output equals the same record run alone, bit for bit
     (bench/attention_bench.m:263-308)."""
