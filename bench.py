@@ -5,6 +5,7 @@ records, 4,096 tokens, 24/4 heads, hd 256): the K/V prologue kernel plus the att
 with the fused Q prologue and gate epilogue, on qkv rows already resident in HBM. Steps are
 replayed from a HIP graph (captured once) so host launch cost is not part of the GPU time; the
 timed region is bracketed by torch.cuda.synchronize() and HIP events on the launch stream.
+Untimed passes of the step run for WARM_S seconds before it, so that the device's clocks are up.
 
 Prints one JSON line. `value` is algorithmic TFLOP/s of the whole step (QK^T + PV flops,
 4*hd*nh*pairs); `roofline` covers the attention kernel alone, priced at its time inside the
@@ -29,6 +30,7 @@ sys.path.insert(0, ROOT)
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (published)
 PEAK_HBM_GBS = 8000.0
 CALIB_BYTES = 256 << 20     # bf16 copy used to scale the FETCH_SIZE / WRITE_SIZE counters
+WARM_S = 0.3                # untimed passes of the step before the timed one (device clocks)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
 
 
@@ -398,10 +400,15 @@ def main():
         print(f"profile pass done: copy of {CALIB_BYTES} bytes, 3 steps of {a.config}", flush=True)
         return
     graph = not a.no_graph
-    # An untimed pass of the same shape first: in a fresh process the first timed pass of a HIP
-    # graph ran 8-10% slower than every later one (C1: 87.9 us, then 78.3-80.4 us over the next
-    # 11 passes), whatever eager warm-up preceded it.
-    time_fn(step, a.steps, a.warmup, graph)
+    # Untimed passes of the same shape first, for at least WARM_S seconds: in a fresh process the
+    # first passes of a HIP graph ran 8-12% slower than later ones (C1 at --steps 20: 86.5 us for
+    # the first timed pass after one untimed pass, 76.3 us in the passes a second later), while
+    # the device's clocks come up. The timed pass is then K steps after W warmup steps, as ever.
+    t_warm = time.perf_counter()
+    while True:
+        time_fn(step, a.steps, a.warmup, graph)
+        if time.perf_counter() - t_warm >= WARM_S:
+            break
     ms, wall_ms = time_fn(step, a.steps, a.warmup, graph)
     layer = info.get("layer")
     layer_info = None
