@@ -179,6 +179,15 @@ def time_fn(fn, steps, warmup, graph):
     return start.elapsed_time(end) / steps, wall / steps
 
 
+def warm(fn, steps, warmup, graph):
+    """Untimed passes of fn, as time_fn runs them, for at least WARM_S seconds (device clocks)."""
+    t0 = time.perf_counter()
+    while True:
+        time_fn(fn, steps, warmup, graph)
+        if time.perf_counter() - t0 >= WARM_S:
+            return
+
+
 def cpu_baseline(w, cfg):
     """fp32 CPU oracle (OpenMP) on the same inputs: prologue + attention, median of 5 runs."""
     from cleffa_amd import rope_inv_freq
@@ -223,6 +232,7 @@ def bench_prefix_growth(a):
         _lib.check(lib.clef_hip_prefix_copy(ks.data_ptr(), vs.data_ptr(), src_cap, kd.data_ptr(), vd.data_ptr(),
                                             dst_cap, nkv, hd, keep, s, err, 256), err)
 
+    warm(step, a.steps, a.warmup, not a.no_graph)
     ms, wall_ms = time_fn(step, a.steps, a.warmup, not a.no_graph)
     nbytes = 2 * nkv * hd * 2 * (keep + dst_cap)
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -263,6 +273,7 @@ def bench_omni(a):
     step = lambda: (att.prep(qkv, qn, kn, pos3, planes=planes, status=status), att.attention(*planes, plan, out=out))
     core = lambda: att.attention(*planes, plan, out=out)
     step()
+    warm(step, a.steps, a.warmup, not a.no_graph)
     ms, wall_ms = time_fn(step, a.steps, a.warmup, not a.no_graph)
     core_ms, _ = time_fn(core, a.steps, a.warmup, not a.no_graph)
     flops = 4.0 * 128 * nh * plan.pairs()
@@ -302,6 +313,7 @@ def bench_gemms(a):
     qkv_fn = lambda: gemm(xn, wqkv, Y=qkv, out="bf16", workspace=ws)
     o_fn = lambda: gemm(attn, wo, Y=resid, out="f32", acc=True, workspace=ws)
     qkv_fn(); o_fn()
+    warm(qkv_fn, a.steps, a.warmup, not a.no_graph)
     ms_q, _ = time_fn(qkv_fn, a.steps, a.warmup, not a.no_graph)
     ms_o, _ = time_fn(o_fn, a.steps, a.warmup, not a.no_graph)
     # this build's own QKV kernel (clef_hip_qkv_gemm) on the same operands, with C1's plan: the
@@ -404,11 +416,7 @@ def main():
     # first passes of a HIP graph ran 8-12% slower than later ones (C1 at --steps 20: 86.5 us for
     # the first timed pass after one untimed pass, 76.3 us in the passes a second later), while
     # the device's clocks come up. The timed pass is then K steps after W warmup steps, as ever.
-    t_warm = time.perf_counter()
-    while True:
-        time_fn(step, a.steps, a.warmup, graph)
-        if time.perf_counter() - t_warm >= WARM_S:
-            break
+    warm(step, a.steps, a.warmup, graph)
     ms, wall_ms = time_fn(step, a.steps, a.warmup, graph)
     layer = info.get("layer")
     layer_info = None
