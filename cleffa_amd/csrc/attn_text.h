@@ -289,13 +289,21 @@ __device__ __forceinline__ void text_items(const AttnParams &p, uint16_t *smem, 
         asm volatile("" : "+v"(off));
         __builtin_amdgcn_global_load_lds((const void *)(base + off), (lds_void *)dst, 16, 0, 0);
     };
+    // The key tiles' fills with sc0 set (they miss the CU's vector L1 on the way to LDS: each
+    // tile is read once per CU, and the fills only pushed other lines out of it). Measured,
+    // eight interleaved runs in one call, medians: C1 kernel alone 68.25 -> 67.57 us, step
+    // 76.88 -> 76.52 us; C2 unchanged. The same bit on the Q and gate row loads: +1.1 us.
+    auto lds_fill_g = [&](const char *base, unsigned off, uint16_t *dst) {
+        asm volatile("" : "+v"(off));
+        __builtin_amdgcn_global_load_lds((const void *)(base + off), (lds_void *)dst, 16, 0, 1);
+    };
     auto load_tiles = [&](const Item &s, int kb, uint16_t *Ks, uint16_t *Vs) {
         const char *kt_base = (const char *)(s.kbase + (size_t)kb * HD);
         const char *vt_base = (const char *)(s.vbase + kb);
 #pragma unroll
-        for (int j = 0; j < 4; j++) lds_fill(kt_base, kfo[j], Ks + (wave_s * 4 + j) * 512);
+        for (int j = 0; j < 4; j++) lds_fill_g(kt_base, kfo[j], Ks + (wave_s * 4 + j) * 512);
 #pragma unroll
-        for (int j = 0; j < 4; j++) lds_fill(vt_base, vfo[j], Vs + (wave_s * 4 + j) * 512);
+        for (int j = 0; j < 4; j++) lds_fill_g(vt_base, vfo[j], Vs + (wave_s * 4 + j) * 512);
     };
     // Q or gate rows of the block (128 x 256 bf16 = 64 KB, `off` 0 or HD within the head's
     // 2*HD columns): rows 0-63 into G0, 64-127 into G1, slot s of a half = row s/32, 16-byte
