@@ -452,11 +452,11 @@ def main():
                    **({"lengths": info["lengths"]} if "lengths" in info else {})},
     }
     if core is not None:
-        # The kernel alone and inside the step: three interleaved rounds of the step, the kernel
+        # The kernel alone and inside the step: five interleaved rounds of the step, the kernel
         # alone and the K/V prologue alone (each round K steps), medians, so that all three see
         # the same clock; in-step = step - prologue.
         rounds = {"step": [], "core": [], "prep": []}
-        for _ in range(3):
+        for _ in range(5):
             for k, f in (("step", step), ("core", core), ("prep", prep)):
                 rounds[k].append(time_fn(f, a.steps, a.warmup, graph)[0])
         core_ms = statistics.median(rounds["core"])
