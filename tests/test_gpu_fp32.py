@@ -166,3 +166,28 @@ def test_fp32_persistent_grid_matches_one_item_per_workgroup(monkeypatch):
     monkeypatch.setenv("CLEF_HIP_F32_PERSISTENT", "1")
     out, _ = _run(w)
     assert torch.equal(out.view(torch.int32), one.view(torch.int32))
+
+
+FP32_GEOMETRIES = [(24, 4), (16, 4), (8, 2), (4, 1), (6, 2), (12, 4), (16, 8), (10, 5), (2, 2), (5, 1), (14, 2),
+                   (9, 1), (24, 2), (7, 1)]
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_fp32_random_pass(seed):
+    """Seeded random packed passes in the FP32 mode (ragged records around the 16-row workgroups
+    and 32-key tiles; group widths 1-12, split over two waves per head up to 6 and as head chunks
+    above 8; with and without the norms, rotary and gate) against float64 within the FP32
+    bound."""
+    rng = np.random.default_rng(5000 + seed)
+    n = int(rng.integers(1, 5))
+    lengths = [int(x) for x in rng.choice([1, 2, 15, 16, 17, 31, 33, 64, 65, 127, 129, 300], size=n)]
+    nh, nkv = FP32_GEOMETRIES[int(rng.integers(len(FP32_GEOMETRIES)))]
+    norm = bool(rng.integers(2))
+    n_rot = 64 if norm and rng.integers(3) else 0
+    gate = bool(rng.integers(2))
+    _say(f"[fp32] random seed {seed}: lengths {lengths} heads {nh}/{nkv} norm {norm} rot {n_rot} gate {gate}")
+    w = workloads.text_inputs(lengths, nh, nkv, n_rot=n_rot, seed=seed, norm=norm)
+    w.update(gate=gate, theta=1e7)
+    w = _fp32(w)
+    out, _ = _run(w)
+    _check_fp32(out.cpu().numpy(), w, what=f"random {seed}")

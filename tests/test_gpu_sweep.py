@@ -16,7 +16,7 @@ from tests.helpers import assert_close, oracle_text
 
 pytestmark = pytest.mark.gpu
 
-GEOMETRIES = [(24, 4), (16, 4), (8, 2), (4, 1), (6, 2), (12, 4)]
+GEOMETRIES = [(24, 4), (16, 4), (8, 2), (4, 1), (6, 2), (12, 4), (16, 8), (10, 5), (32, 4), (8, 8), (2, 1)]
 
 
 def _say(*a):
@@ -37,7 +37,7 @@ def _case(seed):
     return lengths, nh, nkv, norm, n_rot, gate, n_wg
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(40))
 def test_random_text_pass(seed):
     lengths, nh, nkv, norm, n_rot, gate, n_wg = _case(seed)
     _say(f"[sweep] seed {seed}: lengths {lengths} heads {nh}/{nkv} norm {norm} rot {n_rot} gate {gate} n_wg {n_wg}")
