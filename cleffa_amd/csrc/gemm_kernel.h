@@ -204,8 +204,8 @@ __global__ __launch_bounds__(C::THREADS, 1) void qkv_gemm_kernel(Params p) {
     const int nk = p.K / BK, nsteps = nk * KS;
     for (int q = 0; q < STAGES - 1 && q < nk; q++) fill(q, q);
     auto enter_slice = [&](int q) {   // slice q may be read once this returns
-        const int ahead = min(STAGES - 2, nk - 1 - q);
-        wait_fills_barrier<FILLS>(ahead);
+        if constexpr (STAGES == 2) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        else wait_fills_barrier<FILLS>(min(STAGES - 2, nk - 1 - q));
         if (q + STAGES - 1 < nk) fill(q + STAGES - 1, (q + STAGES - 1) % STAGES);
     };
     auto step_addr = [&](int s, const unsigned *a) {
@@ -215,19 +215,23 @@ __global__ __launch_bounds__(C::THREADS, 1) void qkv_gemm_kernel(Params p) {
     enter_slice(0);
     read_frags<NT, MT, RS>(r0, step_addr(0, wa), step_addr(0, xa));
     wait_frags<0>(r0);
-    auto step = [&](int s, bf16x8 (&cur)[FR], bf16x8 (&nxt)[FR]) {
-        const bool more = s + 1 < nsteps;
-        if (more) {
-            if ((s + 1) % KS == 0) enter_slice((s + 1) / KS);
-            read_frags<NT, MT, RS>(nxt, step_addr(s + 1, wa), step_addr(s + 1, xa));
-        }
-        products(cur);
-        if (more) wait_frags<0>(nxt);
-    };
-    for (int s = 0; s < nsteps; s += 2) {
-        step(s, r0, r1);
-        if (s + 1 < nsteps) step(s + 1, r1, r0);
+    // Two steps per slice (K is a multiple of 64, so nsteps is even and at least 2). The loop
+    // body is branch-free apart from the slice's fill: with conditional steps inside it the
+    // compiler split the accumulators' live ranges and copied them on every pass.
+    static_assert(KS == 2, "two 32-deep steps per slice");
+    for (int s = 0; s < nsteps - 2; s += 2) {
+        read_frags<NT, MT, RS>(r1, step_addr(s + 1, wa), step_addr(s + 1, xa));
+        products(r0);
+        wait_frags<0>(r1);
+        enter_slice(s / 2 + 1);
+        read_frags<NT, MT, RS>(r0, step_addr(s + 2, wa), step_addr(s + 2, xa));
+        products(r1);
+        wait_frags<0>(r0);
     }
+    read_frags<NT, MT, RS>(r1, step_addr(nsteps - 1, wa), step_addr(nsteps - 1, xa));
+    products(r0);
+    wait_frags<0>(r1);
+    products(r1);
 
     // ---- epilogue: bf16 C tile into LDS (every wave has left the stage buffers)
     __syncthreads();
